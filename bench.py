@@ -1,0 +1,334 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused per-token DiT layer ops on one MI355X.
+
+Default workload: the per-block chain over T = 201,436
+sparse tokens (a thickened sphere shell on a 128^3 grid), width 1536,
+12 x 128 heads, hidden 6144, f16 storage:
+
+    timestep embedding [1, 256]
+    -> LayerNorm + adaLN modulate          x[T,1536] -> h[T,1536]
+    -> QK RMSNorm + 3D RoPE from coords    q,k[T,12,128] -> q',k'
+    -> GELU-tanh(+bias)                    u[T,6144] -> g[T,6144]
+    -> gated residual                      x + gate*y -> out[T,1536]
+
+One step = one pass of this chain; inputs are resident in HBM before the
+timed region. value = algorithmic HBM bytes of the chain / time (GB/s);
+52,240 bytes per token (6,144 + 12,304 + 24,576 + 9,216).
+
+Prints ONE JSON line on stdout; per-op and per-config detail goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "trellis2-mojo_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "fused-layer HBM GB/s (% of MI355X peak) and tokens/s at width 1536, 1 GPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
+    p.add_argument("--all-configs", action="store_true", help="also time BASELINE configs 1-4 (stderr)")
+    p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
+    return p.parse_args()
+
+
+class Chain:
+    """Device buffers and launches of the config-5 chain."""
+
+    C, H, D, F = 1536, 12, 128, 6144
+
+    def __init__(self, dev, dtype):
+        import numpy as np
+        import torch
+
+        from t2h import nn, ops, workloads
+
+        self.torch, self.ops, self.np = torch, ops, np
+        coords, offsets = workloads.config5()
+        self.coords_np = coords
+        self.T = T = coords.shape[0]
+        C, H, D, F = self.C, self.H, self.D, self.F
+        g = torch.Generator(device=dev).manual_seed(5)
+
+        def rn(shape, std=1.0, mean=0.0, dt=dtype):
+            return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std + mean).to(dt)
+
+        self.coords = torch.from_numpy(coords).to(dev)
+        self.offsets = torch.from_numpy(offsets).to(dev)
+        self.t = torch.rand((1,), generator=g, device=dev) * 1000.0            # t * 1000 (flow_euler.mojo:168)
+        self.x = rn((T, C))
+        self.shift, self.scale, self.gate = rn((1, C), 0.1, dt=torch.float32), rn((1, C), 0.1, dt=torch.float32), \
+            rn((1, C), 0.1, dt=torch.float32)
+        self.h = torch.empty_like(self.x)
+        self.q, self.k = rn((T, H, D)), rn((T, H, D))
+        self.qo, self.ko = torch.empty_like(self.q), torch.empty_like(self.k)
+        self.gq, self.gk = rn((H, D), 0.02, 1.0, torch.float32), rn((H, D), 0.02, 1.0, torch.float32)
+        self.freqs = nn.rope_freqs(D)
+        self.u = rn((T, F))
+        self.bias = rn((F,), 0.02, dt=torch.float32)
+        self.gout = torch.empty_like(self.u)
+        self.y = rn((T, C))
+        self.res = torch.empty_like(self.x)
+        self.temb = None
+        e = 2 if dtype != torch.float32 else 4
+        self.bytes = {  # algorithmic HBM bytes per launch
+            "timestep": 1 * (4 + 256 * 4),
+            "ln_modulate": 2 * T * C * e + 2 * C * 4,
+            "qk_rmsnorm_rope": 4 * T * C * e + T * 16 + 2 * H * D * 4,
+            "gelu_tanh_bias": 2 * T * F * e + F * 4,
+            "gate_residual": 3 * T * C * e + C * 4,
+        }
+        self.chain_bytes = (6144 + 12304 + 24576 + 9216) * T   # BASELINE.md byte model
+
+    def op(self, name):
+        o = self.ops
+        if name == "timestep":
+            return lambda: o.timestep_embedding(self.t, 256)
+        if name == "ln_modulate":
+            return lambda: o.ln_modulate(self.x, 1e-6, shift=self.shift, scale=self.scale, offsets=self.offsets,
+                                         out=self.h)
+        if name == "qk_rmsnorm_rope":
+            return lambda: o.qk_rmsnorm_rope(q=self.q, k=self.k, gamma_q=self.gq, gamma_k=self.gk, freqs=self.freqs,
+                                             coords=self.coords, q_out=self.qo, k_out=self.ko)
+        if name == "gelu_tanh_bias":
+            return lambda: o.activation(self.u, o.ACT_GELU_TANH, bias=self.bias, out=self.gout)
+        if name == "gate_residual":
+            return lambda: o.gate_residual(self.x, self.y, gate=self.gate, offsets=self.offsets, out=self.res)
+        raise KeyError(name)
+
+    ORDER = ["timestep", "ln_modulate", "qk_rmsnorm_rope", "gelu_tanh_bias", "gate_residual"]
+
+    def step(self):
+        for n in self.ORDER:
+            self.op(n)()
+
+
+def time_region(torch, fn, steps):
+    """Events on torch's current stream (the stream every t2h op enqueues on)."""
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e)
+
+
+def time_op(torch, fn, reps, flush=None):
+    """Median per-launch ms; with `flush`, the device caches are flushed
+    (>= 1 GiB streamed) before each launch and only the launch is timed."""
+    times = []
+    for _ in range(reps):
+        if flush is not None:
+            flush()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
+
+
+def cpu_baseline(chain, target_s):
+    """The C oracle (the reference's CPU path restated; serial LN/modulate/
+    phase build/gate, OpenMP GELU/RMSNorm/rotate chunks) over a bounded sample
+    of the same chain: f32 math on the f16-rounded inputs of the first
+    `n` tokens; n grows until one pass takes about target_s."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    torch = chain.torch
+    threads = min(os.cpu_count() or 1, 16)
+    C, H, D, F = chain.C, chain.H, chain.D, chain.F
+
+    def run(n):
+        x = chain.x[:n].float().cpu().numpy()
+        q, k = chain.q[:n].float().cpu().numpy(), chain.k[:n].float().cpu().numpy()
+        u, y = chain.u[:n].float().cpu().numpy(), chain.y[:n].float().cpu().numpy()
+        co = chain.coords_np[:n]
+        sh, sc, gt = (a.cpu().numpy() for a in (chain.shift, chain.scale, chain.gate))
+        gq, gk, bias = chain.gq.cpu().numpy(), chain.gk.cpu().numpy(), chain.bias.cpu().numpy()
+        tt = chain.t.cpu().numpy()
+        off = np.array([0, n], np.int64)
+        freqs = orc.rope_freqs(D)
+        t0 = time.perf_counter()
+        orc.timestep_embedding(tt, 256)
+        orc.ln_modulate(x, sh, sc, offsets=off, eps=1e-6)
+        ph = orc.rope_phases_from_coords(co, D, freqs)
+        orc.qk_rms_rope(q, k, gq, gk, ph, nthreads=threads)
+        orc.gelu_tanh_bias(u, bias, nthreads=threads)
+        orc.gate_residual(x, y, gt, offsets=off)
+        return time.perf_counter() - t0
+
+    n = 2048
+    dt = run(n)
+    n = int(min(chain.T, max(n, n * target_s / max(dt, 1e-3))))
+    dt = run(n)
+    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one pass of the config-5 chain over the first {n} of {chain.T} tokens "
+                      f"(f32 C oracle on f16-rounded inputs, {dt:.1f} s; OpenMP {threads} threads for "
+                      f"GELU/RMSNorm/RoPE-rotate as the reference's parallelize, the rest serial)",
+            "seconds": dt, "tokens": n, "gbs_equiv": chain.chain_bytes / chain.T * n / dt / 1e9}
+
+
+def other_configs(torch, dev):
+    """BASELINE configs 1-4, each op alone, warm and cold (caches flushed)."""
+    import numpy as np
+
+    from t2h import nn, ops, workloads
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    rn = lambda shape, std=1.0, mean=0.0, dt=torch.float32: (
+        torch.randn(shape, generator=g, device=dev) * std + mean).to(dt)
+    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    flush = lambda: flush_buf.zero_()
+    res = {}
+
+    def rec(name, fn, nbytes, tokens, reps=30):
+        for _ in range(3):
+            fn()
+        warm = time_op(torch, fn, reps)
+        cold = time_op(torch, fn, reps, flush)
+        res[name] = {"bytes": nbytes, "tokens": tokens, "warm_ms": warm, "cold_ms": cold,
+                     "warm_gbs": nbytes / warm / 1e6, "cold_gbs": nbytes / cold / 1e6,
+                     "cold_pct_peak": nbytes / cold / 1e6 / HBM_PEAK_GBS * 100,
+                     "tokens_per_s_cold": tokens / cold * 1e3}
+        log(f"  {name:<28s} warm {warm*1e3:8.1f} us {nbytes/warm/1e6:8.1f} GB/s | cold {cold*1e3:8.1f} us "
+            f"{nbytes/cold/1e6:8.1f} GB/s ({nbytes/cold/1e6/HBM_PEAK_GBS*100:5.1f}%)")
+
+    C = 1536
+    x = rn((4096, C)); sh = rn((C,), 0.1); sc = rn((C,), 0.1); out = torch.empty_like(x)
+    rec("c1_ln_modulate_f32", lambda: ops.ln_modulate(x, 1e-6, shift=sh, scale=sc, out=out), 2 * 4096 * C * 4 + 2 * C * 4, 4096)
+    q, k = rn((4096, 12, 128)), rn((4096, 12, 128)); gq, gk = rn((12, 128), 0.02, 1.0), rn((12, 128), 0.02, 1.0)
+    qo, ko = torch.empty_like(q), torch.empty_like(k); fr = nn.rope_freqs(128)
+    rec("c2_qk_rms_rope_f32", lambda: ops.qk_rmsnorm_rope(q=q, k=k, gamma_q=gq, gamma_k=gk, freqs=fr, grid_res=16,
+                                                           q_out=qo, k_out=ko), 4 * 4096 * C * 4 + 2 * C * 4, 4096)
+    del x, out, q, k, qo, ko
+    h = rn((32768, 6144), dt=torch.float16); b = rn((6144,), 0.02); ho = torch.empty_like(h)
+    rec("c3a_gelu_bias_f16", lambda: ops.activation(h, 3, bias=b, out=ho), 2 * 32768 * 6144 * 2 + 6144 * 4, 32768, 20)
+    del h, ho
+    xr, yr = rn((32768, C), dt=torch.float16), rn((32768, C), dt=torch.float16); gt = rn((C,), 0.1)
+    ro = torch.empty_like(xr)
+    rec("c3b_gated_residual_f16", lambda: ops.gate_residual(xr, yr, gate=gt, out=ro), 3 * 32768 * C * 2 + C * 4, 32768)
+    del xr, yr, ro
+    coords, offsets = workloads.config4()
+    T = coords.shape[0]
+    co, off = torch.from_numpy(coords).to(dev), torch.from_numpy(offsets).to(dev)
+    f4 = rn((T, C)); s4, c4 = rn((2, C), 0.1), rn((2, C), 0.1); o4 = torch.empty_like(f4)
+    rec("c4_sparse_ln_mod_f32", lambda: ops.ln_modulate(f4, 1e-6, shift=s4, scale=c4, offsets=off, out=o4),
+        2 * T * C * 4 + 2 * 2 * C * 4 + 16, T)
+    q4, k4 = rn((T, 12, 128)), rn((T, 12, 128)); q4o, k4o = torch.empty_like(q4), torch.empty_like(k4)
+    rec("c4_sparse_qk_rope_f32", lambda: ops.qk_rmsnorm_rope(q=q4, k=k4, gamma_q=gq, gamma_k=gk, freqs=fr, coords=co,
+                                                              q_out=q4o, k_out=k4o), 4 * T * C * 4 + T * 16, T)
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (the per-token ops are row-"
+              f"independent; see DESIGN.md for how rows would shard). Got --gpus {args.gpus}.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from t2h import ops
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    ops.device_init(0)
+    dtype = torch.float16
+    chain = Chain(dev, dtype)
+    log(f"config5: T={chain.T} tokens, chain bytes {chain.chain_bytes/1e9:.3f} GB/step")
+
+    if args.op:
+        fn = chain.op(args.op)
+        for _ in range(args.warmup):
+            fn()
+        ms = time_region(torch, fn, args.steps)
+        log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {chain.bytes[args.op]/(ms/args.steps)/1e6:.1f} GB/s")
+        return
+
+    for _ in range(args.warmup):
+        chain.step()
+    torch.cuda.synchronize()
+    ms = time_region(torch, chain.step, args.steps)
+    ms_step = ms / args.steps
+    gbs = chain.chain_bytes / ms_step / 1e6
+    tok_s = chain.T / ms_step * 1e3
+    log(f"chain: {ms_step*1e3:.1f} us/step, {gbs:.1f} GB/s ({gbs/HBM_PEAK_GBS*100:.1f}% of peak), "
+        f"{tok_s/1e6:.1f} M tokens/s")
+
+    # per-op launch durations (same stream, same buffers), live
+    per_op = {}
+    for n in Chain.ORDER:
+        fn = chain.op(n)
+        fn()
+        reps = max(10, args.steps)
+        t_ms = time_region(torch, fn, reps) / reps
+        per_op[n] = {"us": t_ms * 1e3, "bytes": chain.bytes[n], "gbs": chain.bytes[n] / t_ms / 1e6}
+        log(f"  {n:<18s} {t_ms*1e3:8.1f} us  {chain.bytes[n]/t_ms/1e6:8.1f} GB/s "
+            f"({chain.bytes[n]/t_ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
+    dom = "gelu_tanh_bias"
+    ach = per_op[dom]["gbs"]
+    traffic = None
+    tr_path = os.path.join(ROOT, "profiles", "traffic_c5.json")
+    if os.path.exists(tr_path):
+        try:
+            traffic = json.load(open(tr_path)).get(dom)
+        except Exception:
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
+                "bytes_per_launch": chain.bytes[dom], "launch_us": round(per_op[dom]["us"], 2)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(chain, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.0f} tokens/s on {cpu['cores']} threads ({cpu['sample']})")
+    if args.all_configs:
+        log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
+        other = other_configs(torch, dev)
+        with open(os.path.join(ROOT, "gpurun_out", "configs.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out"))
+                  else os.devnull, "w") as f:
+            json.dump(other, f, indent=1)
+
+    out = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "tokens_per_s": round(tok_s, 0), "pct_of_peak": round(gbs / HBM_PEAK_GBS * 100, 2),
+        "config": {"workload": "BASELINE config 5: per-block chain timestep-embed -> LN+adaLN modulate -> "
+                               "QK RMSNorm+3D RoPE (int coords) -> GELU-tanh+bias -> gated residual, "
+                               "f16 storage / f32 math",
+                   "tokens": chain.T, "width": 1536, "heads": 12, "head_dim": 128, "hidden": 6144,
+                   "grid": "128^3 thickened sphere shell", "bytes_per_token": 52240},
+        "per_op": {k: {"us": round(v["us"], 2), "gbs": round(v["gbs"], 1)} for k, v in per_op.items()},
+        "roofline": roofline,
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,280 @@
+/*
+ * t2h.h — C ABI of libt2h.so: MI355X (gfx950) kernels for the fused per-token
+ * ops of TRELLIS.2's flow-matching DiT blocks (LayerNorm + adaLN modulate,
+ * multi-head QK RMSNorm, 3D RoPE from voxel coordinates, GELU-tanh + bias,
+ * gated residual, sinusoidal timestep embedding), over dense token rows and
+ * SparseTensor feature rows.
+ *
+ * Callers: the reference's Mojo host code through
+ * `external_call["t2h_...", Int32](...)` behind its TRELLIS2_GPU switch
+ * (trellis2_mojo/gpu/context.mojo:168-182), and the Python `t2h` package
+ * (ctypes) used by the tests and bench.py.
+ *
+ * Conventions (every entry point):
+ *   - Returns int32 status: T2H_OK (0) or a negative T2H_E* code; the message
+ *     is in t2h_last_error() (thread-local, valid until the next call on the
+ *     same thread).
+ *   - Pointers are DEVICE pointers unless the name ends in `_host`. The
+ *     t2h_h_* functions take HOST pointers only.
+ *   - `stream` is a hipStream_t (NULL = the default stream). Device entry
+ *     points only enqueue work: no allocation, no synchronisation, no host
+ *     reads of device data. They are stateless and reentrant.
+ *   - `dtype` (T2H_F32 / T2H_F16 / T2H_BF16) is the storage type of the token
+ *     tensors; all arithmetic is f32. Parameter vectors (shift, scale, gate,
+ *     bias, gamma, weight) are always f32, as in the reference.
+ *   - Output may alias input (in place) wherever the entry point says so.
+ *   - rows == 0 is a valid no-op (empty tensors).
+ *
+ * Batch map — which row of a [B, C] parameter array applies to token row r
+ * (the reference's `batch_broadcast_map`, sparse/basic.mojo:149-155, and the
+ * dense [N, L, C] broadcast of modules/nn.mojo:660-689):
+ *   offsets != NULL      b(r) = the b with offsets[b] <= r < offsets[b+1]
+ *                        (int64 device [nbatch+1], VarLenTensor offsets);
+ *   else rows_per_batch  b(r) = r / rows_per_batch   (dense [N, L, C], L);
+ *   else                 b(r) = 0.
+ * Parameter row b starts at param + b * p_stride (p_stride 0 = cols), so the
+ * six adaLN chunks can be read in place from one [B, 6C] modulation tensor.
+ */
+#ifndef T2H_H
+#define T2H_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T2H_VERSION 10000 /* 1.0.0 */
+
+/* storage types */
+#define T2H_F32 0
+#define T2H_F16 1
+#define T2H_BF16 2
+
+/* status codes */
+#define T2H_OK 0
+#define T2H_EINVAL (-1)          /* bad argument (shape mismatch, NULL, range) */
+#define T2H_EUNSUPPORTED (-2)    /* valid but unsupported shape/dtype */
+#define T2H_EHIP (-3)            /* HIP runtime error */
+#define T2H_EBATCH_ORDER (-4)    /* coords: batches not ordered/contiguous */
+#define T2H_EBATCH_RANGE (-5)    /* coords: batch index out of range */
+#define T2H_EDEVICE (-6)         /* device is not gfx950 */
+
+/* LayerNorm epilogue modes (gpu/block.mojo:47-83 modes 1/2, plus plain) */
+#define T2H_LN_PLAIN 0     /* y = LN(x) */
+#define T2H_LN_MODULATE 1  /* y = LN(x) * (1 + p1[b]) + p0[b]   (p0 shift, p1 scale) */
+#define T2H_LN_AFFINE 2    /* y = LN(x) * p0 + p1               (p0 weight, p1 bias) */
+
+/* activation kinds: modules/nn.mojo:582-585 */
+#define T2H_ACT_RELU 0
+#define T2H_ACT_SILU 1
+#define T2H_ACT_GELU 2
+#define T2H_ACT_GELU_TANH 3
+
+/* binary ops: sparse/tensor.mojo:4-7 */
+#define T2H_OP_ADD 0
+#define T2H_OP_SUB 1
+#define T2H_OP_MUL 2
+#define T2H_OP_DIV 3
+
+/* limits */
+#define T2H_MAX_HALF_HEAD 128      /* head_dim <= 256 */
+#define T2H_MAX_POS_DIM 4
+#define T2H_MAX_TIMESTEP_HALF 512  /* frequency_embedding_size <= 1024 */
+
+/* ---- library ---------------------------------------------------------- */
+int32_t t2h_version(void);
+const char* t2h_last_error(void);
+/* Select `device` and check that it is a gfx950 (MI355X) GPU.
+ * Replaces GpuContext construction + self-test (gpu/context.mojo:116-182). */
+int32_t t2h_device_init(int32_t device);
+
+/* ---- LayerNorm + adaLN modulate -----------------------------------------
+ * Replaces: LayerNorm32.forward (modules/nn.mojo:314-369) fused with
+ * modulate (modules/nn.mojo:660-689) / _mod_shift_scale
+ * (sparse/transformer/modulated.mojo:60-65, batch-gathered), and the Metal
+ * kernel ln_mod_rows (gpu/block.mojo:47-83).
+ * x, out: [rows, cols] of dtype (out may alias x). Per row: mean, biased
+ * variance (two-pass), inv = 1/sqrt(var + eps), n = (x - mean) * inv, then
+ * the `mode` epilogue. For T2H_LN_AFFINE the batch map is ignored. */
+int32_t t2h_ln_modulate(const void* x, void* out, int64_t rows, int32_t cols,
+                        int32_t dtype, float eps, int32_t mode,
+                        const float* p0, const float* p1, int64_t p_stride,
+                        const int64_t* offsets, int32_t nbatch,
+                        int64_t rows_per_batch, void* stream);
+
+/* Modulate alone: out = fl(x * fl(1 + scale[b])) + shift[b], bit-exact with
+ * modules/nn.mojo:680-684 and sparse/transformer/modulated.mojo:60-65. */
+int32_t t2h_modulate(const void* x, void* out, int64_t rows, int32_t cols,
+                     int32_t dtype, const float* shift, const float* scale,
+                     int64_t p_stride, const int64_t* offsets, int32_t nbatch,
+                     int64_t rows_per_batch, void* stream);
+
+/* SparseTensor.elemwise_batch (sparse/basic.mojo:433-436 ->
+ * Tensor._binop_rows sparse/tensor.mojo:205-219): out[r,:] = x[r,:] OP
+ * other[b(r), :]; other_cols == cols or 1 (a per-batch scalar). Bit-exact. */
+int32_t t2h_binop_rows(const void* x, const float* other, void* out,
+                       int64_t rows, int32_t cols, int32_t other_cols,
+                       int32_t dtype, int32_t op, const int64_t* offsets,
+                       int32_t nbatch, int64_t rows_per_batch, void* stream);
+
+/* ---- multi-head QK RMSNorm + 3D RoPE ------------------------------------
+ * Replaces: MultiHeadRMSNorm.forward (sparse/attention/modules.mojo:49-102),
+ * apply_rotary_embedding (modules/rope.mojo:64-88),
+ * SparseRotaryPositionEmbedder.embed (sparse/attention/rope.mojo:128-134) and
+ * the Metal kernels bias_rms_rope_qkv / bias_rms_q
+ * (gpu/attention.mojo:507-563, 596-631), in the order bias -> RMS -> RoPE
+ * (modules/attention.mojo:122-130; sparse/attention/modules.mojo:206-212).
+ *
+ * q_in/k_in/q_out/k_out: [rows, heads, head_dim] with row strides in_stride /
+ * out_stride (elements; 0 = heads*head_dim), so q and k can be views into a
+ * packed qkv [rows, 3, H, D] buffer (stride 3*H*D). Either q or k may be NULL.
+ * In place when q_out == q_in / k_out == k_in.
+ * bias_q/bias_k: [H*D] f32 or NULL. gamma_q/gamma_k: [H, D] f32; both NULL =
+ * no RMS norm. RMS: n = max(sqrt(sum x^2), 1e-12); y = x / n * gamma * scale,
+ * scale = f32(sqrt(f64(head_dim))).
+ * RoPE (use_rope != 0), interleaved pairs (x[2p], x[2p+1]) rotated by
+ * (cos, sin) of slot p; slots p >= pos_dim * freq_dim are identity.
+ * The angle of slot p = pos[p / freq_dim] * freqs_host[p % freq_dim] in f32,
+ * where freqs_host is the caller's HOST table (RotaryPositionEmbedder.freqs,
+ * modules/rope.mojo:33-37; freq_dim <= 128). Position source, first non-NULL:
+ *   phases:  precomputed [phase_rows, D/2, 2] f32, row (r % phase_rows)
+ *   coords:  int32 [rows, coord_cols]; pos[a] = coords[r, 1 + a]
+ *            (sparse/attention/rope.mojo:61)
+ *   grid_res: R > 0, dense 'ij' grid, l = r % R^3 -> (l/R^2, (l/R)%R, l%R)
+ *            (models/sparse_structure_flow.mojo:139-149).
+ */
+int32_t t2h_qk_rmsnorm_rope(const void* q_in, const void* k_in, void* q_out,
+                            void* k_out, int64_t rows, int64_t in_stride,
+                            int64_t out_stride, int32_t heads, int32_t head_dim,
+                            int32_t dtype, const float* bias_q,
+                            const float* bias_k, const float* gamma_q,
+                            const float* gamma_k, int32_t use_rope,
+                            const float* freqs_host, int32_t freq_dim,
+                            int32_t pos_dim, const float* phases,
+                            int64_t phase_rows, const int32_t* coords,
+                            int32_t coord_cols, int32_t grid_res, void* stream);
+
+/* In place on a packed qkv GEMM output [rows, 3, H, D]: + bias (all three),
+ * RMS q/k, RoPE q/k — exactly the Metal kernel bias_rms_rope_qkv
+ * (gpu/attention.mojo:507-563; consts layout [3HD bias][HD gq][HD gk]).
+ * bias may be NULL; gamma_q/gamma_k NULL = no RMS. */
+int32_t t2h_qkv_bias_rmsnorm_rope(void* qkv, int64_t rows, int32_t heads,
+                                  int32_t head_dim, int32_t dtype,
+                                  const float* bias, const float* gamma_q,
+                                  const float* gamma_k, int32_t use_rope,
+                                  const float* freqs_host, int32_t freq_dim,
+                                  int32_t pos_dim, const float* phases,
+                                  int64_t phase_rows, const int32_t* coords,
+                                  int32_t coord_cols, int32_t grid_res,
+                                  void* stream);
+
+/* Phase table [rows, head_dim/2, 2] f32 (cos, sin): replaces
+ * RotaryPositionEmbedder.forward (modules/rope.mojo:39-61; positions f32
+ * [rows, pos_dim]) and SparseRotaryPositionEmbedder._compute_phases
+ * (sparse/attention/rope.mojo:48-66; int32 coords). Source: positions, else
+ * coords, else grid_res. */
+int32_t t2h_rope_phases(float* phases_out, int64_t rows, int32_t head_dim,
+                        const float* freqs_host, int32_t freq_dim,
+                        int32_t pos_dim, const float* positions,
+                        const int32_t* coords, int32_t coord_cols,
+                        int32_t grid_res, void* stream);
+
+/* ---- activation (+ bias) -------------------------------------------------
+ * Replaces: activation(x, kind) (modules/nn.mojo:588-647) applied to a
+ * linear's output with its bias (nn.mojo:123-133), i.e. act(x + bias[col]),
+ * and the Metal kernel gelu_tanh_bias (gpu/linear.mojo:662-684).
+ * x, out: [rows, cols] (out may alias x); bias [cols] f32 or NULL. */
+int32_t t2h_activation(const void* x, void* out, const float* bias,
+                       int64_t rows, int32_t cols, int32_t dtype, int32_t kind,
+                       void* stream);
+
+/* ---- gated residual ------------------------------------------------------
+ * Replaces: `y + _gate(h, g)` (modules/transformer/modulated.mojo:22-33,
+ * 60-69, 192-200), `x + h.elemwise_batch(gate, MUL)`
+ * (sparse/transformer/modulated.mojo:214-226) and the Metal kernel
+ * gate_add_bias_rows (gpu/block.mojo:86-110):
+ *   out = x + fl(fl(h + bias) * gate[b(r)])       (each step one rounding)
+ * bias NULL: no bias step; gate NULL: ungated (x + h); x NULL: out = the gated
+ * term alone (`_gate`). out may alias x or h. Bit-exact with the reference. */
+int32_t t2h_gate_residual(const void* x, const void* h, void* out,
+                          const float* bias, const float* gate,
+                          int64_t p_stride, int64_t rows, int32_t cols,
+                          int32_t dtype, const int64_t* offsets,
+                          int32_t nbatch, int64_t rows_per_batch, void* stream);
+
+/* Fused block join: x_out = x + fl(fl(h + bias) * gate[b]) (as above, stored
+ * in dtype), then y_out = LN(x_out) with the `mode` epilogue (as
+ * t2h_ln_modulate, p0/p1). One HBM pass instead of two. x_out may alias x. */
+int32_t t2h_gate_residual_ln_modulate(
+    const void* x, const void* h, void* x_out, void* y_out, const float* bias,
+    const float* gate, int64_t gate_stride, float eps, int32_t mode,
+    const float* p0, const float* p1, int64_t p_stride, int64_t rows,
+    int32_t cols, int32_t dtype, const int64_t* offsets, int32_t nbatch,
+    int64_t rows_per_batch, void* stream);
+
+/* ---- timestep embedding --------------------------------------------------
+ * Replaces TimestepEmbedder.timestep_embedding
+ * (models/sparse_structure_flow.mojo:60-76): t [n] f32 -> out [n, dim]:
+ * half = dim/2, freq_j = exp(-f32(log(max_period)) * j / half) (f32),
+ * out[:, j] = cos(t * freq_j), out[:, half + j] = sin(t * freq_j); odd dim
+ * leaves a zero last column. dim/2 <= T2H_MAX_TIMESTEP_HALF. */
+int32_t t2h_timestep_embedding(const float* t, void* out, int64_t n,
+                               int32_t dim, int32_t dtype, double max_period,
+                               void* stream);
+
+/* ---- SparseTensor layout ---------------------------------------------------
+ * Replaces SparseTensor._cal_offsets (sparse/basic.mojo:321-339): offsets
+ * [nbatch+1] int64 from coords[:, 0] (int32 [rows, coord_cols]).
+ * first_bad (int64 device scalar) receives INT64_MAX when valid, else
+ * (r << 1) | kind for the first offending row r (kind 0: batch below the
+ * previous row's — not ordered/contiguous; kind 1: batch < 0 or >= nbatch),
+ * the reference's two `raise` branches in its row order. Offsets are
+ * meaningful only when first_bad == INT64_MAX. */
+int32_t t2h_coords_to_offsets(const int32_t* coords, int64_t rows,
+                              int32_t coord_cols, int32_t nbatch,
+                              int64_t* offsets, int64_t* first_bad,
+                              void* stream);
+
+/* Modulation.chunks, share_mod branch (sparse/transformer/modulated.mojo:
+ * 41-48): m[r, j] = mod[r, j] + modulation[j] over [n, width] (f32). */
+int32_t t2h_modulation_add(const float* mod, const float* modulation, float* m,
+                           int64_t n, int64_t width, void* stream);
+
+/* ---- host-pointer convenience (synchronous) ------------------------------
+ * For the unchanged Tensor[F32] API (host memory in, fresh host tensor out,
+ * modules/nn.mojo:314-320): copy in, run the device entry point on the
+ * default stream, copy out. These allocate device memory per call; the
+ * device-pointer entry points above are the hot path. All f32. */
+int32_t t2h_h_ln_modulate(const float* x_host, float* out_host, int64_t rows,
+                          int32_t cols, float eps, int32_t mode,
+                          const float* p0_host, const float* p1_host,
+                          const int64_t* offsets_host, int32_t nbatch,
+                          int64_t rows_per_batch);
+int32_t t2h_h_qk_rmsnorm_rope(const float* q_host, const float* k_host,
+                              float* q_out_host, float* k_out_host,
+                              int64_t rows, int32_t heads, int32_t head_dim,
+                              const float* gamma_q_host,
+                              const float* gamma_k_host, int32_t use_rope,
+                              const float* freqs_host, int32_t freq_dim,
+                              int32_t pos_dim, const float* phases_host,
+                              int64_t phase_rows, const int32_t* coords_host,
+                              int32_t coord_cols, int32_t grid_res);
+int32_t t2h_h_activation(const float* x_host, float* out_host,
+                         const float* bias_host, int64_t rows, int32_t cols,
+                         int32_t kind);
+int32_t t2h_h_gate_residual(const float* x_host, const float* h_host,
+                            float* out_host, const float* bias_host,
+                            const float* gate_host, int64_t rows, int32_t cols,
+                            const int64_t* offsets_host, int32_t nbatch,
+                            int64_t rows_per_batch);
+int32_t t2h_h_timestep_embedding(const float* t_host, float* out_host,
+                                 int64_t n, int32_t dim, double max_period);
+int32_t t2h_h_coords_to_offsets(const int32_t* coords_host, int64_t rows,
+                                int32_t coord_cols, int32_t nbatch,
+                                int64_t* offsets_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* T2H_H */

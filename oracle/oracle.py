@@ -1,0 +1,371 @@
+"""numpy binding of the C oracle (oracle.c) — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker. The product path (libt2h.so and the
+t2h package) never imports it.
+
+Every wrapper takes/returns float32 numpy arrays (int32 for coords, int64 for
+offsets) and raises ValueError where the reference raises `Error`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+ACT_RELU, ACT_SILU, ACT_GELU, ACT_GELU_TANH = 0, 1, 2, 3   # modules/nn.mojo:582-585
+OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3                # sparse/tensor.mojo:4-7
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i64 = ctypes.c_int64
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile (gcc)."""
+    cmd = ["make", "-C", _HERE] + (["-B"] if force else [])
+    subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.orc_rng_next_u64.restype = ctypes.c_uint64
+        L.orc_rng_next_f64.restype = ctypes.c_double
+        L.orc_rng_normal.restype = ctypes.c_double
+        L.orc_rmsnorm_scale.restype = ctypes.c_float
+        L.orc_rope_freqs.restype = ctypes.c_int64
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        for name in ("orc_layernorm", "orc_modulate", "orc_cal_offsets", "orc_binop_rows",
+                     "orc_mod_shift_scale", "orc_multihead_rmsnorm",
+                     "orc_rope_phases_from_positions", "orc_rope_phases_from_coords",
+                     "orc_apply_rotary", "orc_rope_rotate", "orc_activation"):
+            getattr(L, name).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    if a.dtype == np.float32:
+        return a.ctypes.data_as(_f32p)
+    if a.dtype == np.int32:
+        return a.ctypes.data_as(_i32p)
+    if a.dtype == np.int64:
+        return a.ctypes.data_as(_i64p)
+    raise TypeError(a.dtype)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- seeded inputs (rng.mojo) --------------------------------------------
+class Rng(ctypes.Structure):
+    """xorshift64* seeded through splitmix64 (trellis2_mojo/rng.mojo:17-46)."""
+    _fields_ = [("state", ctypes.c_uint64)]
+
+    def __init__(self, seed: int):
+        super().__init__()
+        lib().orc_rng_init(ctypes.byref(self), ctypes.c_uint64(seed))
+
+    def next_u64(self) -> int:
+        return lib().orc_rng_next_u64(ctypes.byref(self))
+
+    def next_f64(self) -> float:
+        return lib().orc_rng_next_f64(ctypes.byref(self))
+
+    def normal(self) -> float:
+        return lib().orc_rng_normal(ctypes.byref(self))
+
+    def randn(self, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        lib().orc_randn(ctypes.byref(self), _p(out), _i64(out.size),
+                        ctypes.c_double(mean), ctypes.c_double(std))
+        return out
+
+    def uniform(self, shape, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        lib().orc_uniform(ctypes.byref(self), _p(out), _i64(out.size),
+                          ctypes.c_double(lo), ctypes.c_double(hi))
+        return out
+
+
+def randn(seed: int, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    return Rng(seed).randn(shape, mean, std)
+
+
+# ---- ops -------------------------------------------------------------------
+def layernorm(x, eps: float = 1e-5, affine: bool = False, w=None, b=None) -> np.ndarray:
+    x = _f32(x)
+    c = x.shape[-1]
+    out = np.empty_like(x)
+    if affine:
+        w, b = _f32(w), _f32(b)
+        if w.size != c or b.size != c:
+            raise ValueError("LayerNorm32: affine params mismatch")
+    else:
+        w = b = np.zeros(1, np.float32)
+    rc = lib().orc_layernorm(_p(x), _p(out), _i64(x.size // c), _i64(c),
+                             ctypes.c_double(eps), int(affine), _p(w), _p(b))
+    if rc:
+        raise ValueError("LayerNorm32: last dim mismatch")
+    return out
+
+
+def modulate(x, shift, scale) -> np.ndarray:
+    """x [N, L, C], shift/scale [N, C] (modules/nn.mojo:660-689)."""
+    x, shift, scale = _f32(x), _f32(shift), _f32(scale)
+    n, l, c = x.shape
+    if shift.size != n * c or scale.size != n * c:
+        raise ValueError("modulate: shift/scale shape mismatch")
+    out = np.empty_like(x)
+    lib().orc_modulate(_p(x), _p(shift), _p(scale), _p(out), _i64(n), _i64(l), _i64(c))
+    return out
+
+
+def cal_offsets(coords, batch_size: int) -> np.ndarray:
+    coords = np.ascontiguousarray(coords, dtype=np.int32)
+    off = np.zeros(batch_size + 1, np.int64)
+    rc = lib().orc_cal_offsets(_p(coords), _i64(coords.shape[0]), _i64(coords.shape[1]),
+                               _i64(batch_size), _p(off))
+    if rc == -1:
+        raise ValueError("SparseTensor: batches must be ordered/contiguous")
+    if rc == -2:
+        raise ValueError("SparseTensor: batch index out of range")
+    return off
+
+
+def batch_broadcast_map(offsets) -> np.ndarray:
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    out = np.empty(int(offsets[-1]), np.int64)
+    lib().orc_batch_broadcast_map(_p(offsets), _i64(offsets.size - 1), _p(out))
+    return out
+
+
+def binop_rows(x, other, row_map, op: int) -> np.ndarray:
+    x, other = _f32(x), _f32(other)
+    row_map = np.ascontiguousarray(row_map, dtype=np.int64)
+    rows = x.shape[0]
+    c = x.size // rows if rows else 0
+    oc = other.size // other.shape[0]
+    out = np.empty_like(x)
+    if lib().orc_binop_rows(_p(x), _p(other), _p(row_map), _p(out), _i64(rows), _i64(c), _i64(oc), op):
+        raise ValueError("Tensor._binop_rows: incompatible row size")
+    return out
+
+
+def binop_scalar(x, v: float, op: int) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_binop_scalar(_p(x), ctypes.c_float(v), _p(out), _i64(x.size), op)
+    return out
+
+
+def binop_flat(x, y, op: int) -> np.ndarray:
+    x, y = _f32(x), _f32(y)
+    if x.size != y.size:
+        raise ValueError("Tensor binop: size mismatch")
+    out = np.empty_like(x)
+    lib().orc_binop_flat(_p(x), _p(y), _p(out), _i64(x.size), op)
+    return out
+
+
+def mod_shift_scale(h, shift, scale, offsets) -> np.ndarray:
+    h, shift, scale = _f32(h), _f32(shift), _f32(scale)
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    rows, c = h.shape
+    out = np.empty_like(h)
+    lib().orc_mod_shift_scale(_p(h), _p(shift), _p(scale), _p(offsets), _i64(offsets.size - 1),
+                              _p(out), _i64(rows), _i64(c))
+    return out
+
+
+def modulation_add(mod, modulation) -> np.ndarray:
+    mod, modulation = _f32(mod), _f32(modulation)
+    out = np.empty_like(mod)
+    lib().orc_modulation_add(_p(mod), _p(modulation), _p(out), _i64(mod.shape[0]), _i64(mod.shape[1]))
+    return out
+
+
+def multihead_rmsnorm(x, gamma, nthreads: int = 1) -> np.ndarray:
+    x, gamma = _f32(x), _f32(gamma)
+    h, d = x.shape[-2], x.shape[-1]
+    rows = x.size // (h * d)
+    out = np.empty_like(x)
+    lib().orc_multihead_rmsnorm(_p(x), _p(gamma), _p(out), _i64(rows), _i64(h), _i64(d), int(nthreads))
+    return out
+
+
+def rmsnorm_scale(d: int) -> float:
+    return lib().orc_rmsnorm_scale(_i64(d))
+
+
+def rope_freqs(head_dim: int, dim: int = 3, freq_lo: float = 1.0, freq_hi: float = 10000.0) -> np.ndarray:
+    if head_dim % 2:
+        raise ValueError("RotaryPositionEmbedder: head_dim must be even")
+    fd = head_dim // 2 // dim
+    out = np.zeros(max(fd, 1), np.float32)
+    lib().orc_rope_freqs(_i64(head_dim), _i64(dim), ctypes.c_double(freq_lo), ctypes.c_double(freq_hi), _p(out))
+    return out[:fd]
+
+
+def rope_phases_from_positions(pos, head_dim: int, freqs) -> np.ndarray:
+    pos, freqs = _f32(pos), _f32(freqs)
+    l, dim = pos.shape
+    out = np.empty((l, head_dim // 2, 2), np.float32)
+    lib().orc_rope_phases_from_positions(_p(pos), _i64(l), _i64(dim), _i64(head_dim),
+                                         _p(freqs if freqs.size else np.zeros(1, np.float32)),
+                                         _i64(freqs.size), _p(out))
+    return out
+
+
+def rope_phases_from_coords(coords, head_dim: int, freqs, dim: int = 3) -> np.ndarray:
+    coords = np.ascontiguousarray(coords, dtype=np.int32)
+    freqs = _f32(freqs)
+    n, ncols = coords.shape
+    out = np.empty((n, head_dim // 2, 2), np.float32)
+    rc = lib().orc_rope_phases_from_coords(_p(coords), _i64(n), _i64(ncols), _i64(dim), _i64(head_dim),
+                                           _p(freqs if freqs.size else np.zeros(1, np.float32)),
+                                           _i64(freqs.size), _p(out))
+    if rc:
+        raise ValueError("rope: coords must have dim+1 columns")
+    return out
+
+
+def grid_positions(r: int) -> np.ndarray:
+    out = np.empty((r * r * r, 3), np.float32)
+    lib().orc_grid_positions(_i64(r), _p(out))
+    return out
+
+
+def apply_rotary(x, phases) -> np.ndarray:
+    x, phases = _f32(x), _f32(phases)
+    n, l, h, d = x.shape
+    if phases.shape[0] != l or phases.shape[1] != d // 2:
+        raise ValueError("apply_rotary_embedding: phases shape mismatch")
+    out = np.empty_like(x)
+    lib().orc_apply_rotary(_p(x), _p(phases), _p(out), _i64(n), _i64(l), _i64(h), _i64(d))
+    return out
+
+
+def rope_rotate(feats, phases, nthreads: int = 1) -> np.ndarray:
+    feats, phases = _f32(feats), _f32(phases)
+    n = feats.shape[0]
+    d = feats.shape[-1]
+    h = feats.size // (n * d) if n else 0
+    out = np.empty_like(feats)
+    lib().orc_rope_rotate(_p(feats), _p(phases), _p(out), _i64(n), _i64(h), _i64(d), int(nthreads))
+    return out
+
+
+def activation(x, kind: int, nthreads: int = 1) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    if lib().orc_activation(_p(x), _p(out), _i64(x.size), int(kind), int(nthreads)):
+        raise ValueError("unknown activation")
+    return out
+
+
+def add_bias(x, bias) -> np.ndarray:
+    x, bias = _f32(x), _f32(bias)
+    c = bias.size
+    out = np.empty_like(x)
+    lib().orc_add_bias(_p(x), _p(bias), _p(out), _i64(x.size // c), _i64(c))
+    return out
+
+
+def gate(x, g) -> np.ndarray:
+    """x [N, L, C] * g [N, C] (modules/transformer/modulated.mojo:22-33)."""
+    x, g = _f32(x), _f32(g)
+    n, l, c = x.shape
+    out = np.empty_like(x)
+    lib().orc_gate(_p(x), _p(g), _p(out), _i64(n), _i64(l), _i64(c))
+    return out
+
+
+def timestep_embedding(t, dim: int = 256, max_period: float = 10000.0) -> np.ndarray:
+    t = _f32(t).reshape(-1)
+    out = np.empty((t.size, dim), np.float32)
+    lib().orc_timestep_embedding(_p(t), _i64(t.size), _i64(dim), ctypes.c_double(max_period), _p(out))
+    return out
+
+
+def round_f16(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_round_f16(_p(x), _p(out), _i64(x.size))
+    return out
+
+
+def round_bf16(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_round_bf16(_p(x), _p(out), _i64(x.size))
+    return out
+
+
+# ---- compositions used by the parity tests --------------------------------
+def ln_modulate(x, shift, scale, offsets=None, eps: float = 1e-6) -> np.ndarray:
+    """norm (non-affine) then batch-gathered modulate: the block's
+    `modulate(norm1(x), shift, scale)` / `_mod_shift_scale(norm1(h), ...)`."""
+    x = _f32(x)
+    rows, c = x.shape
+    n = layernorm(x, eps=eps)
+    shift = _f32(shift).reshape(-1, c)
+    scale = _f32(scale).reshape(-1, c)
+    if offsets is None:
+        offsets = np.array([0, rows], np.int64)
+    return mod_shift_scale(n, shift, scale, offsets)
+
+
+def qk_rms_rope(q, k, gamma_q, gamma_k, phases, bias_q=None, bias_k=None,
+                use_rms: bool = True, use_rope: bool = True, nthreads: int = 1):
+    """bias -> MultiHeadRMSNorm -> RoPE on q and k [rows, H, D] with per-row
+    phases [rows, D/2, 2] (sparse/attention/modules.mojo:206-212,
+    gpu/attention.mojo:507-563 order)."""
+    q, k = _f32(q), _f32(k)
+    if bias_q is not None:
+        q = (q + _f32(bias_q).reshape(q.shape[1:])).astype(np.float32)
+    if bias_k is not None:
+        k = (k + _f32(bias_k).reshape(k.shape[1:])).astype(np.float32)
+    if use_rms:
+        q = multihead_rmsnorm(q, gamma_q, nthreads)
+        k = multihead_rmsnorm(k, gamma_k, nthreads)
+    if use_rope:
+        q = rope_rotate(q, phases, nthreads)
+        k = rope_rotate(k, phases, nthreads)
+    return q, k
+
+
+def gelu_tanh_bias(h, bias=None, nthreads: int = 1) -> np.ndarray:
+    h = _f32(h)
+    v = add_bias(h, bias) if bias is not None else h
+    return activation(v, ACT_GELU_TANH, nthreads)
+
+
+def gate_residual(x, h, gate_rows, offsets=None, bias=None) -> np.ndarray:
+    """x + fl(fl(h [+ bias]) * gate[b(r)]) — the block's `y + _gate(h, g)` /
+    `x + h.elemwise_batch(gate, MUL)`, with gpu/block.mojo:86-110's
+    out-linear bias fold when bias is given."""
+    x, h = _f32(x), _f32(h)
+    rows, c = x.shape
+    if bias is not None:
+        h = add_bias(h, bias)
+    if gate_rows is not None:
+        g = _f32(gate_rows).reshape(-1, c)
+        if offsets is None:
+            offsets = np.array([0, rows], np.int64)
+        h = binop_rows(h, g, batch_broadcast_map(offsets), OP_MUL)
+    return binop_flat(x, h, OP_ADD)

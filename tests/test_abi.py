@@ -1,0 +1,75 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/t2h.h declares, and rejects invalid arguments before touching the
+device (no compute call is made here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from t2h import _build, _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "t2h.h")
+
+
+def declared_symbols():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(t2h_\w+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_build.LIB_PATH):
+        _build.build()
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in t2h.h but not exported"
+    assert sorted(_lib.EXPORTED) == syms, "ctypes signature table out of sync with t2h.h"
+
+
+def test_version(lib):
+    assert lib.t2h_version() == 10000
+
+
+def test_validation_without_device(lib):
+    p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    assert lib.t2h_ln_modulate(p, p, 4, 1536, 7, 1e-6, 0, None, None, 0, None, 1, 0, None) == _lib.T2H_EINVAL
+    assert b"bad dtype" in lib.t2h_last_error()
+    assert lib.t2h_ln_modulate(p, p, 4, 1536, 0, 1e-6, 1, None, None, 0, None, 1, 0, None) == _lib.T2H_EINVAL
+    assert b"needs p0 and p1" in lib.t2h_last_error()
+    assert lib.t2h_activation(p, p, None, 4, 8, 0, 9, None) == _lib.T2H_EINVAL
+    assert lib.t2h_last_error() == b"unknown activation"
+    assert lib.t2h_binop_rows(p, p, p, 4, 8, 3, 0, 0, None, 1, 0, None) == _lib.T2H_EINVAL
+    assert b"incompatible row size" in lib.t2h_last_error()
+    freqs = np.ones(21, np.float32)
+    rc = lib.t2h_qk_rmsnorm_rope(p, p, p, p, 4, 0, 0, 12, 127, 0, None, None, None, None, 1,
+                                 freqs.ctypes.data, 21, 3, None, 0, None, 0, 16, None)
+    assert rc == _lib.T2H_EINVAL and b"head_dim must be even" in lib.t2h_last_error()
+    rc = lib.t2h_qk_rmsnorm_rope(p, p, p, p, 4, 0, 0, 12, 128, 0, None, None, None, None, 1,
+                                 freqs.ctypes.data, 21, 3, None, 0, None, 0, 0, None)
+    assert rc == _lib.T2H_EINVAL and b"needs phases, coords or grid_res" in lib.t2h_last_error()
+    rc = lib.t2h_timestep_embedding(p, p, 4, 4096, 0, 10000.0, None)
+    assert rc == _lib.T2H_EUNSUPPORTED
+
+
+def test_empty_is_a_noop(lib):
+    # rows == 0 returns before any device work
+    assert lib.t2h_ln_modulate(None, None, 0, 1536, 0, 1e-6, 0, None, None, 0, None, 1, 0, None) == 0
+    assert lib.t2h_activation(None, None, None, 0, 6144, 1, 3, None) == 0
+    assert lib.t2h_gate_residual(None, None, None, None, None, 0, 0, 1536, 1, None, 1, 0, None) == 0
+    assert lib.t2h_last_error() == b""
+
+
+def test_oracle_not_linked(lib):
+    """The product library does not depend on the oracle."""
+    import subprocess
+
+    out = subprocess.run(["readelf", "-d", _build.LIB_PATH], stdout=subprocess.PIPE, text=True).stdout
+    assert "oracle" not in out

@@ -1,0 +1,198 @@
+"""GPU parity: multi-head QK RMSNorm + 3D RoPE (+ qkv bias) and the phase
+builder, through the C ABI, against the C oracle
+(sparse/attention/modules.mojo:37-102; modules/rope.mojo:17-88;
+sparse/attention/rope.mojo:20-134; gpu/attention.mojo:507-631).
+Metric and tolerances: tests/_parity.py."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from _parity import assert_close, host, max_err, storage_round, to_dev
+from t2h import nn, ops, sparse, workloads
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _gammas(h, d, seed):
+    return orc.randn(seed, (h, d), mean=1.0, std=0.02), orc.randn(seed + 1, (h, d), mean=1.0, std=0.02)
+
+
+def test_config2_dense_grid_f32(dev):
+    """fp32 Q,K [4096,12,128], gamma 1+N(0,0.02), 16^3 grid
+    positions, base 10000, 21 freqs/axis + identity pad slot 63."""
+    rows, h, d = 4096, 12, 128
+    q, k = orc.randn(1, (rows, h, d)), orc.randn(2, (rows, h, d))
+    gq, gk = _gammas(h, d, 3)
+    freqs = orc.rope_freqs(d)
+    assert freqs.size == 21
+    phases = orc.rope_phases_from_positions(orc.grid_positions(16), d, freqs)
+    wq, wk = orc.qk_rms_rope(q, k, gq, gk, phases)
+    qo, ko = ops.qk_rmsnorm_rope(q=to_dev(q, dev), k=to_dev(k, dev), gamma_q=to_dev(gq, dev),
+                                 gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(d), grid_res=16)
+    assert_close(qo, wq, torch.float32, "config2 q")
+    assert_close(ko, wk, torch.float32, "config2 k")
+
+
+def test_config2_mojo_api(dev):
+    """MultiHeadRMSNorm.forward then apply_rotary_embedding(x [N,L,H,D], phases)
+    with RotaryPositionEmbedder.forward(grid) — the dense MHA order
+    (modules/attention.mojo:122-130)."""
+    l, h, d = 4096, 12, 128
+    q = orc.randn(11, (1, l, h, d))
+    gq, _ = _gammas(h, d, 12)
+    rms = nn.MultiHeadRMSNorm(d, h)
+    rms.gamma = to_dev(gq, dev)
+    emb = nn.RotaryPositionEmbedder(d)
+    pos = to_dev(orc.grid_positions(16), dev)
+    phases = emb.forward(pos)
+    ph_want = orc.rope_phases_from_positions(orc.grid_positions(16), d, orc.rope_freqs(d))
+    assert max_err(phases, ph_want) <= 2e-7, "phase table"
+    got = nn.apply_rotary_embedding(rms.forward(to_dev(q, dev)), phases)
+    want = orc.apply_rotary(orc.multihead_rmsnorm(q, gq), ph_want)
+    assert_close(got, want, torch.float32, "MultiHeadRMSNorm + apply_rotary_embedding")
+    # the grid source and the phase-table source agree
+    g2 = emb.grid_phases(16)
+    assert torch.equal(g2, phases)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_config4_sparse_coords(dev, dtype):
+    """Sparse positions from int coords (config 4 shells, coords up to 63)."""
+    coords, offsets = workloads.config4()
+    t, h, d = coords.shape[0], 12, 128
+    q = storage_round(orc.randn(21, (t, h, d)), dtype)
+    k = storage_round(orc.randn(22, (t, h, d)), dtype)
+    gq, gk = _gammas(h, d, 23)
+    phases = orc.rope_phases_from_coords(coords, d, orc.rope_freqs(d))
+    wq, wk = orc.qk_rms_rope(q, k, gq, gk, phases)
+    qo, ko = ops.qk_rmsnorm_rope(q=to_dev(q, dev, dtype), k=to_dev(k, dev, dtype), gamma_q=to_dev(gq, dev),
+                                 gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(d), coords=to_dev(coords, dev))
+    assert_close(qo, wq, dtype, f"sparse q {dtype}")
+    assert_close(ko, wk, dtype, f"sparse k {dtype}")
+
+
+def test_sparse_embedder_api(dev):
+    """SparseRotaryPositionEmbedder.embed(q, k) after MultiHeadRMSNorm on a
+    128^3 shell (coords up to 127, angles up to 127 rad)."""
+    coords, offsets = workloads.shell_coords(128, 1, 60.0, 1.0, 2.0, seed=9)
+    t, h, d = coords.shape[0], 12, 128
+    q, k = orc.randn(31, (t, h, d)), orc.randn(32, (t, h, d))
+    dq, dk = to_dev(q, dev), to_dev(k, dev)
+    dco = to_dev(coords, dev)
+    emb = sparse.SparseRotaryPositionEmbedder(d)
+    sq = sparse.SparseTensor(dq, dco, 1)
+    sk = sparse.SparseTensor(dk, dco, 1)
+    rq, rk = emb.embed(sq, sk)
+    phases = orc.rope_phases_from_coords(coords, d, orc.rope_freqs(d))
+    assert_close(rq.feats, orc.rope_rotate(q, phases), torch.float32, "embed q")
+    assert_close(rk.feats, orc.rope_rotate(k, phases), torch.float32, "embed k")
+    assert_close(emb._compute_phases(sq), phases, torch.float32, "_compute_phases")
+
+
+def test_packed_qkv_bias(dev):
+    """bias_rms_rope_qkv semantics in place on [rows, 3, H, D]."""
+    rows, h, d = 2048, 12, 128
+    qkv = orc.randn(41, (rows, 3, h, d))
+    bias = orc.randn(42, (3 * h * d,), std=0.1)
+    gq, gk = _gammas(h, d, 43)
+    freqs = orc.rope_freqs(d)
+    phases = orc.rope_phases_from_positions(orc.grid_positions(16)[:rows], d, freqs)
+    b3 = bias.reshape(3, h, d)
+    wq, wk = orc.qk_rms_rope(qkv[:, 0], qkv[:, 1], gq, gk, phases, bias_q=b3[0], bias_k=b3[1])
+    wv = (qkv[:, 2] + b3[2]).astype(np.float32)
+    dq = to_dev(qkv.reshape(rows, -1), dev)
+    ops.qkv_bias_rmsnorm_rope(dq, h, d, bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev),
+                              freqs=freqs, grid_res=16)
+    got = host(dq).reshape(rows, 3, h, d)
+    assert_close(got[:, 0], wq, torch.float32, "packed q")
+    assert_close(got[:, 1], wk, torch.float32, "packed k")
+    assert np.array_equal(got[:, 2], wv), "v bias must be bit-exact"
+
+
+def test_views_into_packed_qkv(dev):
+    """q and k as strided views of a packed qkv buffer, separate outputs."""
+    rows, h, d = 1000, 12, 128
+    qkv = orc.randn(51, (rows, 3, h, d))
+    gq, gk = _gammas(h, d, 52)
+    coords = np.zeros((rows, 4), np.int32)
+    coords[:, 1:] = np.stack([np.arange(rows) % 17, (np.arange(rows) // 17) % 13, np.arange(rows) % 5], 1)
+    dq = to_dev(qkv, dev)
+    qo, ko = ops.qk_rmsnorm_rope(q=dq[:, 0], k=dq[:, 1], gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev),
+                                 freqs=orc.rope_freqs(d), coords=to_dev(coords, dev))
+    phases = orc.rope_phases_from_coords(coords, d, orc.rope_freqs(d))
+    wq, wk = orc.qk_rms_rope(qkv[:, 0], qkv[:, 1], gq, gk, phases)
+    assert_close(qo, wq, torch.float32, "view q")
+    assert_close(ko, wk, torch.float32, "view k")
+    assert np.array_equal(host(dq), qkv), "inputs must be untouched"
+
+
+@pytest.mark.parametrize("h,d", [(16, 64), (4, 128), (8, 64), (20, 128), (6, 96), (2, 32), (12, 256)])
+def test_head_shapes(dev, h, d):
+    """Fast path (D 64/128, H <= 16) and the generic per-(row, head) kernel."""
+    rows = 300
+    q, k = orc.randn(61, (rows, h, d)), orc.randn(62, (rows, h, d))
+    gq, gk = _gammas(h, d, 63)
+    coords = np.zeros((rows, 4), np.int32)
+    coords[:, 1:] = (np.arange(rows * 3).reshape(rows, 3) * 5) % 31
+    freqs = orc.rope_freqs(d)
+    phases = orc.rope_phases_from_coords(coords, d, freqs)
+    wq, wk = orc.qk_rms_rope(q, k, gq, gk, phases)
+    qo, ko = ops.qk_rmsnorm_rope(q=to_dev(q, dev), k=to_dev(k, dev), gamma_q=to_dev(gq, dev),
+                                 gamma_k=to_dev(gk, dev), freqs=freqs, coords=to_dev(coords, dev))
+    assert_close(qo, wq, torch.float32, f"q H={h} D={d}")
+    assert_close(ko, wk, torch.float32, f"k H={h} D={d}")
+
+
+def test_rms_only_and_rope_only(dev):
+    rows, h, d = 512, 12, 128
+    q = orc.randn(71, (rows, h, d))
+    gq, _ = _gammas(h, d, 72)
+    got = nn.MultiHeadRMSNorm(d, h)
+    got.gamma = to_dev(gq, dev)
+    assert_close(got.forward(to_dev(q, dev)), orc.multihead_rmsnorm(q, gq), torch.float32, "rms only")
+    z = np.zeros((4, h, d), np.float32)  # zero heads: the 1e-12 clamp keeps them 0
+    assert np.all(host(got.forward(to_dev(z, dev))) == 0.0)
+    ph = orc.rope_phases_from_positions(orc.grid_positions(8), d, orc.rope_freqs(d))
+    x = orc.randn(73, (1, 512, h, d))
+    out = nn.apply_rotary_embedding(to_dev(x, dev), to_dev(ph, dev))
+    assert_close(out, orc.apply_rotary(x, ph), torch.float32, "rope only")
+
+
+def test_rope_identity_and_norm(dev):
+    """Position 0 is the identity; every pair keeps its norm."""
+    rows, h, d = 256, 12, 128
+    x = orc.randn(81, (rows, h, d))
+    coords = np.zeros((rows, 4), np.int32)
+    out, _ = ops.qk_rmsnorm_rope(q=to_dev(x, dev), freqs=orc.rope_freqs(d), coords=to_dev(coords, dev))
+    assert np.array_equal(host(out), x)
+    coords[:, 1:] = np.random.default_rng(0).integers(0, 128, (rows, 3))
+    out, _ = ops.qk_rmsnorm_rope(q=to_dev(x, dev), freqs=orc.rope_freqs(d), coords=to_dev(coords, dev))
+    o = host(out).reshape(rows, h, d // 2, 2).astype(np.float64)
+    xi = x.reshape(rows, h, d // 2, 2).astype(np.float64)
+    np.testing.assert_allclose(np.hypot(o[..., 0], o[..., 1]), np.hypot(xi[..., 0], xi[..., 1]), rtol=2e-6, atol=1e-6)
+    # pad slot 63 (head_dim 128, 3 x 21 rotated slots) passes through untouched
+    assert np.array_equal(host(out).reshape(rows, h, 64, 2)[:, :, 63], x.reshape(rows, h, 64, 2)[:, :, 63])
+
+
+def test_phase_builder_sources(dev):
+    d = 128
+    freqs = orc.rope_freqs(d)
+    coords, _ = workloads.config4()
+    got = ops.rope_phases(coords.shape[0], d, freqs, coords=to_dev(coords, dev))
+    want = orc.rope_phases_from_coords(coords, d, freqs)
+    assert max_err(got, want) <= 2e-7
+    assert np.array_equal(host(got)[:, 63], np.tile([1.0, 0.0], (coords.shape[0], 1)).astype(np.float32))
+    pos = orc.randn(91, (500, 3), std=30.0)
+    got = ops.rope_phases(500, d, freqs, positions=to_dev(pos, dev))
+    assert max_err(got, orc.rope_phases_from_positions(pos, d, freqs)) <= 2e-7
+
+
+def test_qk_errors(dev):
+    with pytest.raises(ValueError):
+        nn.apply_rotary_embedding(torch.zeros((1, 8, 12, 128), device=dev), torch.zeros((4, 64, 2), device=dev))
+    with pytest.raises(ValueError, match="head_dim must be even"):
+        nn.RotaryPositionEmbedder(127)
+    with pytest.raises(ValueError):  # RoPE without a position source
+        ops.qk_rmsnorm_rope(q=torch.zeros((4, 12, 128), device=dev), freqs=orc.rope_freqs(128))

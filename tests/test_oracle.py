@@ -1,0 +1,279 @@
+"""Pins for the C oracle (CPU only).
+
+Each check is independent of the oracle's own code: the reference's golden
+values (tests/test_runtime.mojo:35-47, tests/parity/test_sparse_basic.mojo),
+float64 closed forms, brute force on tiny inputs, numpy's IEEE float32
+elementwise arithmetic (for the ops that are exact sequences of f32 roundings),
+and identities (RoPE composition / norm preservation, GELU odd part). The
+`mutant` tests show that the checks catch plausible mistakes (a dropped term,
+a wrong sign, an off-by-one variance): the same check applied to a mutated
+restatement fails.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+
+
+# ---- RNG: tests/test_runtime.mojo:35-47 ----------------------------------------
+def test_rng_golden():
+    r = orc.Rng(1337)
+    assert [r.next_u64() for _ in range(3)] == [76748464051394776, 17093336004959153412, 4605377540300676664]
+
+
+def test_randn_deterministic():
+    a, b = orc.Rng(42), orc.Rng(42)
+    ta, tb = a.randn((2, 3, 4)), b.randn((2, 3, 4))
+    assert np.array_equal(ta, tb) and a.state == b.state
+    # Box-Muller closed form from the raw stream (rng.mojo:41-46)
+    r = orc.Rng(7)
+    u = [(r.next_u64() >> 11) * (1.0 / 2 ** 53) for _ in range(2)]
+    want = math.sqrt(-2.0 * math.log(u[0])) * math.cos(6.283185307179586 * u[1])
+    assert orc.Rng(7).normal() == want
+    big = orc.randn(1, (200000,))
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
+
+
+# ---- SparseTensor layout / gather: tests/parity/test_sparse_basic.mojo ----------
+COORDS = np.array([[0, 0, 0, 0], [0, 1, 0, 1], [1, 0, 1, 0], [1, 1, 1, 1], [1, 1, 0, 0]], np.int32)
+FEATS = np.arange(1, 11, dtype=np.float32).reshape(5, 2)
+
+
+def test_sparse_basic_layout():
+    off = orc.cal_offsets(COORDS, 2)
+    assert off.tolist() == [0, 2, 5]                                  # seqlen 2, 3 (:149-158)
+    assert orc.batch_broadcast_map(off).tolist() == [0, 0, 1, 1, 1]   # bm[0]=0, bm[2]=1, bm[4]=1 (:55-59)
+
+
+def test_sparse_basic_elemwise_batch():
+    rm = orc.batch_broadcast_map(orc.cal_offsets(COORDS, 2))
+    b = np.array([[10, 20], [100, 200]], np.float32)
+    y = orc.binop_rows(FEATS, b, rm, orc.OP_ADD).reshape(-1)
+    assert y[0] == 11.0 and y[9] == 210.0                              # (:263-265)
+    assert orc.binop_rows(FEATS, b, rm, orc.OP_MUL).reshape(-1)[1] == 40.0   # (:266-267)
+    s = orc.binop_rows(FEATS, np.array([[10], [100]], np.float32), rm, orc.OP_ADD).reshape(-1)
+    assert s[0] == 11.0 and s[4] == 105.0                              # (:81-84)
+    assert orc.binop_rows(FEATS, b, rm, orc.OP_ADD).reshape(-1)[1] == 22.0   # (:86-89)
+
+
+def test_sparse_contiguity_enforced():
+    bad = np.zeros((2, 4), np.int32)
+    bad[0, 0] = 1
+    with pytest.raises(ValueError, match="ordered/contiguous"):
+        orc.cal_offsets(bad, 2)                                        # (:161-171)
+    bad = np.zeros((2, 4), np.int32)
+    bad[1, 0] = 2
+    with pytest.raises(ValueError, match="out of range"):
+        orc.cal_offsets(bad, 2)
+
+
+def test_offsets_brute_force():
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        nb = int(rng.integers(1, 6))
+        counts = rng.integers(0, 5, nb)
+        coords = np.zeros((counts.sum(), 4), np.int32)
+        coords[:, 0] = np.repeat(np.arange(nb), counts)
+        assert orc.cal_offsets(coords, nb).tolist() == [0] + np.cumsum(counts).tolist()
+        assert orc.batch_broadcast_map(orc.cal_offsets(coords, nb)).tolist() == coords[:, 0].tolist()
+
+
+# ---- exact f32 sequences: numpy float32 ufuncs round each step -------------------
+def test_modulate_exact_f32():
+    x = orc.randn(1, (3, 40, 64))
+    sh, sc = orc.randn(2, (3, 64)), orc.randn(3, (3, 64))
+    want = x * (np.float32(1) + sc[:, None, :]) + sh[:, None, :]
+    assert np.array_equal(orc.modulate(x, sh, sc), want.astype(np.float32))
+    off = np.array([0, 40, 80, 120], np.int64)
+    assert np.array_equal(orc.mod_shift_scale(x.reshape(-1, 64), sh, sc, off), want.reshape(-1, 64))
+
+
+def test_gate_and_residual_exact_f32():
+    x, h = orc.randn(4, (2, 30, 32)), orc.randn(5, (2, 30, 32))
+    g, b = orc.randn(6, (2, 32)), orc.randn(7, (32,))
+    assert np.array_equal(orc.gate(h, g), h * g[:, None, :])
+    off = np.array([0, 30, 60], np.int64)
+    want = x.reshape(-1, 32) + ((h.reshape(-1, 32) + b) * np.repeat(g, 30, axis=0))
+    assert np.array_equal(orc.gate_residual(x.reshape(-1, 32), h.reshape(-1, 32), g, offsets=off, bias=b), want)
+
+
+# ---- LayerNorm: float64 closed form ---------------------------------------------
+def _ln64(x, eps, w=None, b=None):
+    x = x.astype(np.float64)
+    m = x.mean(-1, keepdims=True)
+    v = ((x - m) ** 2).mean(-1, keepdims=True)    # biased variance
+    y = (x - m) / np.sqrt(v + eps)
+    return y * w + b if w is not None else y
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - b) / np.maximum(np.abs(b), 1.0)))
+
+
+def test_layernorm_float64():
+    x = orc.randn(11, (64, 1536), mean=0.7, std=2.5)
+    assert _rel(orc.layernorm(x, 1e-6), _ln64(x, 1e-6)) < 2e-6
+    w, b = orc.randn(12, (1536,), mean=1.0, std=0.1), orc.randn(13, (1536,), std=0.1)
+    assert _rel(orc.layernorm(x, 1e-5, True, w, b), _ln64(x, 1e-5, w, b)) < 2e-6
+    assert _rel(orc.layernorm(x[:, :13], 1e-6), _ln64(x[:, :13], 1e-6)) < 2e-6   # scalar tail
+    assert np.all(orc.layernorm(np.full((2, 24), 5.0, np.float32), 1e-6) == 0.0)
+    t = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (1536,), eps=1e-6).numpy()
+    assert _rel(orc.layernorm(x, 1e-6), t) < 2e-6
+
+
+def test_layernorm_mutant_unbiased_variance_is_caught():
+    x = orc.randn(14, (16, 64))
+    xd = x.astype(np.float64)
+    m = xd.mean(-1, keepdims=True)
+    mutant = (xd - m) / np.sqrt(((xd - m) ** 2).sum(-1, keepdims=True) / 63 + 1e-6)
+    assert _rel(mutant, _ln64(x, 1e-6)) > 1e-3
+    assert _rel(orc.layernorm(x, 1e-6), _ln64(x, 1e-6)) < 2e-6
+
+
+# ---- MultiHeadRMSNorm -------------------------------------------------------------
+def test_rmsnorm_float64():
+    x = orc.randn(21, (100, 12, 128), std=3.0)
+    g = orc.randn(22, (12, 128), mean=1.0, std=0.02)
+    xd = x.astype(np.float64)
+    want = xd / np.maximum(np.linalg.norm(xd, axis=-1, keepdims=True), 1e-12) * g * math.sqrt(128)
+    assert _rel(orc.multihead_rmsnorm(x, g), want) < 2e-6
+    assert orc.rmsnorm_scale(128) == np.float32(math.sqrt(128))
+    # gamma = 1: every head has norm sqrt(D)
+    y = orc.multihead_rmsnorm(x, np.ones((12, 128), np.float32)).astype(np.float64)
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), math.sqrt(128), rtol=1e-6)
+    assert np.all(orc.multihead_rmsnorm(np.zeros((2, 12, 128), np.float32), g) == 0.0)   # 1e-12 clamp
+    # parallel chunks give identical bits (sparse/attention/modules.mojo:96-101)
+    assert np.array_equal(orc.multihead_rmsnorm(x, g, nthreads=4), orc.multihead_rmsnorm(x, g, nthreads=1))
+
+
+# ---- RoPE -------------------------------------------------------------------------
+def test_rope_freqs_closed_form():
+    f = orc.rope_freqs(128)
+    assert f.size == 21                                   # 128 // 2 // 3 (rope.mojo:32)
+    want = 1.0 / 10000.0 ** (np.arange(21) / 21.0)
+    np.testing.assert_allclose(f, want, rtol=3e-7)
+    assert f[0] == 1.0
+    assert orc.rope_freqs(64).size == 10
+
+
+def test_rope_slot_mapping_brute_force():
+    """slot p < 63: axis p // 21, freq p % 21; slot 63 = identity pad (D2)."""
+    d = 128
+    f = orc.rope_freqs(d)
+    pos = np.array([[3.0, 7.0, 11.0], [0.0, 0.0, 0.0], [127.0, 64.0, 1.0]], np.float32)
+    ph = orc.rope_phases_from_positions(pos, d, f)
+    for r in range(3):
+        for p in range(64):
+            if p < 63:
+                ang = np.float32(pos[r, p // 21] * f[p % 21])           # f32 product
+                assert abs(ph[r, p, 0] - math.cos(float(ang))) < 2e-7
+                assert abs(ph[r, p, 1] - math.sin(float(ang))) < 2e-7
+            else:
+                assert ph[r, p, 0] == 1.0 and ph[r, p, 1] == 0.0
+    assert np.all(ph[1, :, 0] == 1.0) and np.all(ph[1, :, 1] == 0.0)   # position 0 = identity
+    co = np.concatenate([np.zeros((3, 1), np.int32), pos.astype(np.int32)], 1)
+    assert np.array_equal(orc.rope_phases_from_coords(co, d, f), ph)    # int coords == float positions
+
+
+def test_grid_positions():
+    g = orc.grid_positions(4)
+    for l in range(64):
+        assert g[l].tolist() == [l // 16, (l // 4) % 4, l % 4]           # meshgrid 'ij'
+
+
+def _rotate64(x, ph):
+    z = x.astype(np.float64).reshape(*x.shape[:-1], -1, 2)
+    c = (z[..., 0] + 1j * z[..., 1]) * (ph[..., 0] + 1j * ph[..., 1])
+    return np.stack([c.real, c.imag], -1).reshape(x.shape)
+
+
+def test_rope_rotate_complex_and_composition():
+    d, n, h = 128, 40, 12
+    x = orc.randn(31, (n, h, d))
+    co = np.zeros((n, 4), np.int32)
+    co[:, 1:] = np.random.default_rng(1).integers(0, 128, (n, 3))
+    f = orc.rope_freqs(d)
+    ph = orc.rope_phases_from_coords(co, d, f)
+    out = orc.rope_rotate(x, ph)
+    assert _rel(out, _rotate64(x, ph.astype(np.float64)[:, None])) < 2e-6
+    z, o = x.reshape(n, h, 64, 2).astype(np.float64), out.reshape(n, h, 64, 2).astype(np.float64)
+    np.testing.assert_allclose(np.hypot(o[..., 0], o[..., 1]), np.hypot(z[..., 0], z[..., 1]), rtol=2e-6, atol=1e-7)
+    # composition R(a) R(b) = R(a + b) for integer positions a, b
+    co2 = np.zeros((n, 4), np.int32)
+    co2[:, 1:] = np.random.default_rng(2).integers(0, 64, (n, 3))
+    co3 = co.copy()
+    co3[:, 1:] = co[:, 1:] + co2[:, 1:]
+    two = orc.rope_rotate(orc.rope_rotate(x, ph), orc.rope_phases_from_coords(co2, d, f))
+    one = orc.rope_rotate(x, orc.rope_phases_from_coords(co3, d, f))
+    assert _rel(two, one) < 2e-5
+    # a sign mistake in the rotation breaks composition
+    mut = x.reshape(n, h, 64, 2).copy()
+    re, im = mut[..., 0].copy(), mut[..., 1].copy()
+    c, s = ph[:, None, :, 0], ph[:, None, :, 1]
+    mut[..., 0], mut[..., 1] = re * c + im * s, re * s + im * c
+    assert _rel(mut.reshape(x.shape), _rotate64(x, ph.astype(np.float64)[:, None])) > 1e-2
+
+
+def test_apply_rotary_equals_rotate():
+    """Dense apply_rotary (phases per l) and sparse _rotate (phases per row)
+    use the same per-pair formula: identical bits."""
+    l, h, d = 64, 4, 128
+    x = orc.randn(41, (1, l, h, d))
+    ph = orc.rope_phases_from_positions(orc.grid_positions(4), d, orc.rope_freqs(d))
+    assert np.array_equal(orc.apply_rotary(x, ph)[0], orc.rope_rotate(x[0], ph))
+
+
+# ---- activations ---------------------------------------------------------------
+def test_gelu_tanh_float64_and_identities():
+    x = orc.randn(51, (4096,), std=4.0)
+    t = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="tanh").numpy()
+    g = orc.activation(x, orc.ACT_GELU_TANH)
+    assert _rel(g, t) < 3e-6
+    assert orc.activation(np.zeros(1, np.float32), orc.ACT_GELU_TANH)[0] == 0.0
+    gm = orc.activation(-x, orc.ACT_GELU_TANH)
+    np.testing.assert_allclose(g.astype(np.float64) - gm, x, rtol=1e-5, atol=1e-6)   # odd part is x/2 * 2
+    # mutant: dropping the cubic term is caught by the float64 check
+    xd = x.astype(np.float64)
+    mutant = 0.5 * xd * (1 + np.tanh(0.7978845608028654 * xd))
+    assert _rel(mutant, t) > 1e-3
+    # parallel chunks are bit-identical (nn.mojo:641-646)
+    big = orc.randn(52, (1 << 18,))
+    assert np.array_equal(orc.activation(big, 3, 4), orc.activation(big, 3, 1))
+
+
+def test_other_activations_float64():
+    x = orc.randn(53, (4096,), std=4.0)
+    xt = torch.from_numpy(x).double()
+    assert _rel(orc.activation(x, orc.ACT_RELU), torch.relu(xt).numpy()) == 0.0
+    assert _rel(orc.activation(x, orc.ACT_SILU), torch.nn.functional.silu(xt).numpy()) < 3e-6
+    assert _rel(orc.activation(x, orc.ACT_GELU), torch.nn.functional.gelu(xt).numpy()) < 3e-6
+    with pytest.raises(ValueError, match="unknown activation"):
+        orc.activation(x, 9)
+
+
+# ---- timestep embedding -----------------------------------------------------------
+@pytest.mark.parametrize("dim", [256, 255])
+def test_timestep_float64(dim):
+    t = np.array([0.0, 0.5, 1.0, 999.0], np.float32)
+    e = orc.timestep_embedding(t, dim)
+    half = dim // 2
+    fr = np.exp(-math.log(10000.0) * np.arange(half) / half)
+    ang = t[:, None].astype(np.float64) * fr
+    want = np.concatenate([np.cos(ang), np.sin(ang)], 1)
+    # the f32 angle carries ~|angle| * 6e-8 of rounding: compare within that
+    assert np.max(np.abs(e[:, :2 * half] - want)) < 2e-4
+    assert np.max(np.abs(e[:3, :2 * half] - want[:3])) < 2e-6
+    assert np.all(e[0, :half] == 1.0) and np.all(e[0, half:2 * half] == 0.0)
+    if dim % 2:
+        assert np.all(e[:, -1] == 0.0)
+
+
+# ---- storage rounding -------------------------------------------------------------
+def test_f16_bf16_rounding_matches_torch():
+    x = np.concatenate([orc.randn(61, (100000,), std=1000.0), orc.randn(62, (100000,), std=1e-5),
+                        np.array([65504, 65520, 65519.99, 1e-8, -0.0, np.inf], np.float32)]).astype(np.float32)
+    assert np.array_equal(orc.round_f16(x), torch.from_numpy(x).half().float().numpy())
+    assert np.array_equal(orc.round_bf16(x), torch.from_numpy(x).bfloat16().float().numpy())

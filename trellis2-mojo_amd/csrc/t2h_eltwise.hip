@@ -1,0 +1,419 @@
+// Elementwise token-row ops: activation(+bias), gated residual, modulate,
+// batch-broadcast binop, sinusoidal timestep embedding, coords -> batch
+// offsets, share_mod modulation add.
+//
+// Row-tiled layout: a 256-thread block covers 256 * V columns (V = 16 B of
+// storage per thread) of RPT consecutive rows. Per-column parameters (bias)
+// are loaded once per thread; per-batch parameter rows (gate, shift/scale,
+// `other`) are reloaded only when the tile's row crosses a batch boundary
+// (the batch of a row is block-uniform). All RPT rows are loaded before any
+// is computed so each thread keeps RPT x 16 B per stream in flight. No
+// integer division per element: the column comes from the thread index.
+//
+// Reference: modules/nn.mojo:588-647 (activation), 660-689 (modulate);
+// modules/transformer/modulated.mojo:22-33 (_gate); sparse/tensor.mojo:
+// 193-219 (_binop_flat/_binop_rows); sparse/transformer/modulated.mojo:60-65;
+// gpu/block.mojo:86-110 (gate_add_bias_rows); gpu/linear.mojo:662-684
+// (gelu_tanh_bias); models/sparse_structure_flow.mojo:60-76 (timestep);
+// sparse/basic.mojo:321-339 (_cal_offsets).
+#include "t2h_device.h"
+#include "t2h_internal.h"
+
+namespace t2h {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kRpt = 4;  // rows per thread
+
+// ---- activations (f32 math) ------------------------------------------------
+// GELU-tanh: 0.5*v*(1+tanh(z)) == v * sigmoid(2z) == v / (1 + exp(-2z)), with
+// z = 0.7978845608028654*(v + 0.044715*v^3). exp via v_exp_f32 (exp2) and the
+// reciprocal via v_rcp_f32: a few ulp, no cancellation near z = 0 (unlike
+// (1-e)/(1+e)), and saturates cleanly (exp overflow -> 0, underflow -> v).
+__device__ __forceinline__ float gelu_tanh_f(float v) {
+    constexpr float k0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;  // -2*sqrt(2/pi)*log2(e)
+    constexpr float k1 = k0 * 0.044715f;
+    const float v2 = v * v;
+    const float arg = v * __builtin_fmaf(k1, v2, k0);   // -2z * log2(e)
+    const float e = __builtin_amdgcn_exp2f(arg);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float silu_f(float v) {
+    const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float gelu_erf_f(float v) {
+    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+template <int KIND> __device__ __forceinline__ float act_f(float v) {
+    if constexpr (KIND == T2H_ACT_RELU) return v > 0.0f ? v : 0.0f;
+    else if constexpr (KIND == T2H_ACT_SILU) return silu_f(v);
+    else if constexpr (KIND == T2H_ACT_GELU) return gelu_erf_f(v);
+    else return gelu_tanh_f(v);
+}
+
+// Vector (V = 16 B) or scalar (V = 1) access to V elements of a row.
+template <typename T, int V>
+__device__ __forceinline__ void ld(const T* p, float* f) {
+    if constexpr (V == 1) f[0] = ld1(p);
+    else load_elems<T, V, true>(p, f);
+}
+template <typename T, int V>
+__device__ __forceinline__ void st(T* p, const float* f) {
+    if constexpr (V == 1) st1(p, f[0]);
+    else store_elems<T, V, true>(p, f);
+}
+template <int V>
+__device__ __forceinline__ void ldp(const float* p, float* f) {
+    if constexpr (V == 1) f[0] = *p;
+    else load_params<V>(p, f);
+}
+
+struct Tile {
+    int64_t col0;
+    int64_t r0;
+    int nrows;
+};
+
+template <int V>
+__device__ __forceinline__ bool tile_of(const EltArgs& a, Tile& t) {
+    t.col0 = ((int64_t)blockIdx.y * kBlock + threadIdx.x) * V;
+    t.r0 = (int64_t)blockIdx.x * kRpt;
+    const int64_t left = a.rows - t.r0;
+    t.nrows = left < kRpt ? (int)left : kRpt;
+    return t.col0 < a.cols;
+}
+
+// ---- activation(x + bias) ----------------------------------------------------
+template <typename T, int V, int KIND>
+__global__ __launch_bounds__(kBlock) void act_kernel(EltArgs a) {
+    Tile t;
+    if (!tile_of<V>(a, t)) return;
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    T* __restrict__ o = static_cast<T*>(a.out);
+    float bias[V];
+    if (a.bias) ldp<V>(a.bias + t.col0, bias);
+    float v[kRpt][V];
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k)
+        if (k < t.nrows) ld<T, V>(x + (t.r0 + k) * a.cols + t.col0, v[k]);
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k) {
+        if (k >= t.nrows) break;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const float u = a.bias ? add_rn(v[k][i], bias[i]) : v[k][i];   // linear bias: acc + b
+            v[k][i] = act_f<KIND>(u);
+        }
+        st<T, V>(o + (t.r0 + k) * a.cols + t.col0, v[k]);
+    }
+}
+
+// ---- out = x + fl(fl(h + bias) * gate[b]) ------------------------------------
+template <typename T, int V>
+__global__ __launch_bounds__(kBlock) void gate_res_kernel(EltArgs a) {
+    Tile t;
+    if (!tile_of<V>(a, t)) return;
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* __restrict__ h = static_cast<const T*>(a.h);
+    T* __restrict__ o = static_cast<T*>(a.out);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    float bias[V], g[V];
+    if (a.bias) ldp<V>(a.bias + t.col0, bias);
+    int32_t cur = -1;
+    float hv[kRpt][V], xv[kRpt][V];
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k) {
+        if (k < t.nrows) {
+            const int64_t off = (t.r0 + k) * a.cols + t.col0;
+            ld<T, V>(h + off, hv[k]);
+            if (x) ld<T, V>(x + off, xv[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k) {
+        if (k >= t.nrows) break;
+        const int64_t r = t.r0 + k;
+        if (a.gate) {
+            const int32_t b = bm.batch_of(r);
+            if (b != cur) { ldp<V>(a.gate + b * a.p_stride + t.col0, g); cur = b; }
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            float u = a.bias ? add_rn(hv[k][i], bias[i]) : hv[k][i];
+            if (a.gate) u = mul_rn(u, g[i]);
+            hv[k][i] = x ? add_rn(xv[k][i], u) : u;
+        }
+        st<T, V>(o + r * a.cols + t.col0, hv[k]);
+    }
+}
+
+// ---- out = fl(fl(x * fl(1 + scale[b])) + shift[b]) ---------------------------
+template <typename T, int V>
+__global__ __launch_bounds__(kBlock) void modulate_kernel(EltArgs a) {
+    Tile t;
+    if (!tile_of<V>(a, t)) return;
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    T* __restrict__ o = static_cast<T*>(a.out);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    float sc1[V], sh[V];
+    int32_t cur = -1;
+    float v[kRpt][V];
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k)
+        if (k < t.nrows) ld<T, V>(x + (t.r0 + k) * a.cols + t.col0, v[k]);
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k) {
+        if (k >= t.nrows) break;
+        const int64_t r = t.r0 + k;
+        const int32_t b = bm.batch_of(r);
+        if (b != cur) {
+            ldp<V>(a.gate + b * a.p_stride + t.col0, sc1);
+            ldp<V>(a.shift + b * a.p_stride + t.col0, sh);
+#pragma unroll
+            for (int i = 0; i < V; ++i) sc1[i] = add_rn(1.0f, sc1[i]);
+            cur = b;
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[k][i] = add_rn(mul_rn(v[k][i], sc1[i]), sh[i]);
+        st<T, V>(o + r * a.cols + t.col0, v[k]);
+    }
+}
+
+// ---- out = x OP other[b] (other row of cols, or one scalar per batch) ---------
+__device__ __forceinline__ float apply_op(float x, float y, int op) {
+    switch (op) {
+        case T2H_OP_ADD: return add_rn(x, y);
+        case T2H_OP_SUB: return sub_rn(x, y);
+        case T2H_OP_MUL: return mul_rn(x, y);
+        default: return __fdiv_rn(x, y);
+    }
+}
+
+template <typename T, int V>
+__global__ __launch_bounds__(kBlock) void binop_kernel(EltArgs a) {
+    Tile t;
+    if (!tile_of<V>(a, t)) return;
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    T* __restrict__ o = static_cast<T*>(a.out);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    const bool full = a.other_cols == a.cols;
+    const int64_t ost = full ? a.p_stride : 1;
+    float ov[V];
+    int32_t cur = -1;
+    float v[kRpt][V];
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k)
+        if (k < t.nrows) ld<T, V>(x + (t.r0 + k) * a.cols + t.col0, v[k]);
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k) {
+        if (k >= t.nrows) break;
+        const int64_t r = t.r0 + k;
+        const int32_t b = bm.batch_of(r);
+        if (b != cur) {
+            if (full) {
+                ldp<V>(a.gate + b * ost + t.col0, ov);
+            } else {
+                const float s = a.gate[b * ost];
+#pragma unroll
+                for (int i = 0; i < V; ++i) ov[i] = s;
+            }
+            cur = b;
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[k][i] = apply_op(v[k][i], ov[i], a.kind);
+        st<T, V>(o + r * a.cols + t.col0, v[k]);
+    }
+}
+
+// ---- timestep embedding --------------------------------------------------------
+struct FreqTable {
+    float f[T2H_MAX_TIMESTEP_HALF];
+};
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void timestep_kernel(const float* __restrict__ tv, T* __restrict__ out,
+                                                          int64_t n, int32_t dim, FreqTable ft) {
+    const int half = dim / 2;
+    const int per_row = half + (dim & 1);
+    const int64_t total = n * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+        const int64_t r = i / per_row;
+        const int j = (int)(i % per_row);
+        if (j >= half) {  // odd dim: zero last column
+            st1(out + r * dim + dim - 1, 0.0f);
+            continue;
+        }
+        const float angle = __fmul_rn(tv[r], ft.f[j]);
+        float s, c;
+        sincosf(angle, &s, &c);
+        st1(out + r * dim + j, c);
+        st1(out + r * dim + half + j, s);
+    }
+}
+
+// ---- coords -> offsets ---------------------------------------------------------
+__global__ void offsets_init_kernel(unsigned long long* first_bad) { *first_bad = 0x7FFFFFFFFFFFFFFFull; }
+
+// Thread r (0 <= r <= rows) owns the batch boundaries between row r-1 and r:
+// offsets[bb] = r for every bb in (b(r-1), b(r)], with b(-1) = -1 and
+// b(rows) = nbatch. Rows of one batch are contiguous, so each offsets entry
+// has exactly one writer when the coords are valid.
+__global__ __launch_bounds__(kBlock) void offsets_kernel(const int32_t* __restrict__ coords, int64_t rows,
+                                                         int32_t cc, int32_t nbatch, int64_t* __restrict__ offsets,
+                                                         unsigned long long* first_bad) {
+    for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r <= rows; r += (int64_t)gridDim.x * kBlock) {
+        const int64_t prev = r > 0 ? (int64_t)coords[(r - 1) * cc] : -1;
+        int64_t b;
+        if (r < rows) {
+            b = coords[r * cc];
+            if (b < prev) {
+                atomicMin(first_bad, (unsigned long long)((r << 1) | 0));
+                continue;
+            }
+            if (b < 0 || b >= nbatch) {
+                atomicMin(first_bad, (unsigned long long)((r << 1) | 1));
+                continue;
+            }
+        } else {
+            b = nbatch;
+        }
+        int64_t lo = prev + 1 < 0 ? 0 : prev + 1;
+        int64_t hi = b > nbatch ? nbatch : b;
+        for (int64_t bb = lo; bb <= hi; ++bb) offsets[bb] = r;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void modulation_add_kernel(const float* __restrict__ mod,
+                                                                const float* __restrict__ modulation,
+                                                                float* __restrict__ m, int64_t n, int64_t width) {
+    const int64_t total = n * width;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock)
+        m[i] = add_rn(mod[i], modulation[i % width]);
+}
+
+// ---- launch helpers ------------------------------------------------------------
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T>
+bool vec_ok(const EltArgs& a) {
+    constexpr int V = kPack<T>;
+    return a.cols % V == 0 && al16(a.x) && al16(a.h) && al16(a.out) && al16(a.bias) && al16(a.gate) &&
+           al16(a.shift) && a.p_stride % 4 == 0;
+}
+
+template <int V>
+dim3 tile_grid(const EltArgs& a) {
+    const int64_t rt = (a.rows + kRpt - 1) / kRpt;
+    const int64_t ct = (a.cols + (int64_t)kBlock * V - 1) / ((int64_t)kBlock * V);
+    return dim3((unsigned)rt, (unsigned)ct);
+}
+
+template <template <typename, int> class K, typename T>
+struct Unused {};
+
+#define T2H_DISPATCH_DTYPE(DT, FN, ...)                                \
+    switch (DT) {                                                      \
+        case T2H_F32: return FN<float>(__VA_ARGS__);                   \
+        case T2H_F16: return FN<_Float16>(__VA_ARGS__);                \
+        default: return FN<__bf16>(__VA_ARGS__);                       \
+    }
+
+template <typename T, int KIND>
+hipError_t act_typed_kind(const EltArgs& a, hipStream_t s) {
+    constexpr int V = kPack<T>;
+    if (vec_ok<T>(a))
+        hipLaunchKernelGGL((act_kernel<T, V, KIND>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL((act_kernel<T, 1, KIND>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t act_typed(const EltArgs& a, hipStream_t s) {
+    switch (a.kind) {
+        case T2H_ACT_RELU: return act_typed_kind<T, T2H_ACT_RELU>(a, s);
+        case T2H_ACT_SILU: return act_typed_kind<T, T2H_ACT_SILU>(a, s);
+        case T2H_ACT_GELU: return act_typed_kind<T, T2H_ACT_GELU>(a, s);
+        default: return act_typed_kind<T, T2H_ACT_GELU_TANH>(a, s);
+    }
+}
+
+template <typename T>
+hipError_t gate_res_typed(const EltArgs& a, hipStream_t s) {
+    constexpr int V = kPack<T>;
+    if (vec_ok<T>(a))
+        hipLaunchKernelGGL((gate_res_kernel<T, V>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL((gate_res_kernel<T, 1>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t modulate_typed(const EltArgs& a, hipStream_t s) {
+    constexpr int V = kPack<T>;
+    if (vec_ok<T>(a))
+        hipLaunchKernelGGL((modulate_kernel<T, V>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL((modulate_kernel<T, 1>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t binop_typed(const EltArgs& a, hipStream_t s) {
+    constexpr int V = kPack<T>;
+    if (vec_ok<T>(a))
+        hipLaunchKernelGGL((binop_kernel<T, V>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL((binop_kernel<T, 1>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t timestep_typed(const float* t, void* out, int64_t n, int32_t dim, const FreqTable& ft, hipStream_t s) {
+    const int64_t total = n * (dim / 2 + (dim & 1));
+    int64_t grid = (total + kBlock - 1) / kBlock;
+    if (grid < 1) grid = 1;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(timestep_kernel<T>, dim3((unsigned)grid), dim3(kBlock), 0, s, t, static_cast<T*>(out), n, dim, ft);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_activation(const EltArgs& a, hipStream_t s) { T2H_DISPATCH_DTYPE(a.dtype, act_typed, a, s) }
+hipError_t launch_gate_residual(const EltArgs& a, hipStream_t s) { T2H_DISPATCH_DTYPE(a.dtype, gate_res_typed, a, s) }
+hipError_t launch_modulate(const EltArgs& a, hipStream_t s) { T2H_DISPATCH_DTYPE(a.dtype, modulate_typed, a, s) }
+hipError_t launch_binop_rows(const EltArgs& a, hipStream_t s) { T2H_DISPATCH_DTYPE(a.dtype, binop_typed, a, s) }
+
+hipError_t launch_timestep(const float* t, void* out, int64_t n, int32_t dim, int32_t dtype,
+                           const float* freqs_host, hipStream_t s) {
+    FreqTable ft{};
+    for (int j = 0; j < dim / 2; ++j) ft.f[j] = freqs_host[j];
+    T2H_DISPATCH_DTYPE(dtype, timestep_typed, t, out, n, dim, ft, s)
+}
+
+hipError_t launch_offsets(const int32_t* coords, int64_t rows, int32_t coord_cols, int32_t nbatch,
+                          int64_t* offsets, int64_t* first_bad, hipStream_t s) {
+    auto* fb = reinterpret_cast<unsigned long long*>(first_bad);
+    hipLaunchKernelGGL(offsets_init_kernel, dim3(1), dim3(1), 0, s, fb);
+    int64_t grid = (rows + 1 + kBlock - 1) / kBlock;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(offsets_kernel, dim3((unsigned)grid), dim3(kBlock), 0, s, coords, rows, coord_cols, nbatch,
+                       offsets, fb);
+    return hipGetLastError();
+}
+
+hipError_t launch_modulation_add(const float* mod, const float* modulation, float* m, int64_t n, int64_t width,
+                                 hipStream_t s) {
+    int64_t grid = (n * width + kBlock - 1) / kBlock;
+    if (grid < 1) grid = 1;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(modulation_add_kernel, dim3((unsigned)grid), dim3(kBlock), 0, s, mod, modulation, m, n, width);
+    return hipGetLastError();
+}
+
+}  // namespace t2h

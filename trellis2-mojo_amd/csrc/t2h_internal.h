@@ -1,0 +1,119 @@
+// Launcher interface between the C-ABI layer (t2h_api.hip) and the kernel
+// translation units. Arguments arrive validated; launchers only pick a kernel
+// instantiation and a grid, then enqueue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "t2h.h"
+
+namespace t2h {
+
+struct BatchArgs {
+    const int64_t* offsets;
+    int32_t nbatch;
+    int64_t rows_per_batch;
+};
+
+struct LnArgs {
+    const void* x;       // [rows, cols]
+    const void* h;       // residual branch (fused join) or nullptr
+    void* x_out;         // fused join: updated residual stream
+    void* y_out;         // normalised (+ epilogue) output
+    const float* bias;   // join: h bias [cols] or nullptr
+    const float* gate;   // join: gate rows or nullptr
+    int64_t gate_stride;
+    float eps;
+    int32_t mode;        // T2H_LN_*
+    const float* p0;
+    const float* p1;
+    int64_t p_stride;
+    int64_t rows;
+    int32_t cols;
+    int32_t dtype;
+    BatchArgs batch;
+};
+
+// Per-slot RoPE table, passed by value as a kernel argument: slot p rotates
+// pair (2p, 2p+1) by angle pos[axis[p]] * freq[p]; axis -1 = identity slot.
+struct RopeSlots {
+    float freq[T2H_MAX_HALF_HEAD];
+    int8_t axis[T2H_MAX_HALF_HEAD];
+};
+
+struct QkArgs {
+    const void* q_in;
+    const void* k_in;
+    void* q_out;
+    void* k_out;
+    void* v;                 // packed-qkv v (bias only) or nullptr
+    int64_t rows;
+    int64_t in_stride;
+    int64_t out_stride;
+    int32_t heads;
+    int32_t head_dim;
+    int32_t dtype;
+    const float* bias_q;
+    const float* bias_k;
+    const float* bias_v;
+    const float* gamma_q;    // nullptr = no RMS
+    const float* gamma_k;
+    float rms_scale;         // f32(sqrt(f64(head_dim)))
+    int32_t use_rope;
+    int32_t pos_dim;
+    const float* phases;     // position source 1
+    int64_t phase_rows;
+    const int32_t* coords;   // position source 2
+    int32_t coord_cols;
+    int32_t grid_res;        // position source 3
+};
+
+struct PhaseArgs {
+    float* out;
+    int64_t rows;
+    int32_t head_dim;
+    int32_t pos_dim;
+    const float* positions;
+    const int32_t* coords;
+    int32_t coord_cols;
+    int32_t grid_res;
+};
+
+struct EltArgs {
+    const void* x;
+    const void* h;
+    void* out;
+    const float* bias;
+    const float* gate;     // gate rows / modulate scale / binop other
+    const float* shift;    // modulate shift
+    int64_t p_stride;
+    int64_t rows;
+    int32_t cols;
+    int32_t other_cols;    // binop: cols or 1
+    int32_t dtype;
+    int32_t kind;          // activation kind / binop op
+    BatchArgs batch;
+};
+
+// t2h_norm.hip
+hipError_t launch_ln(const LnArgs& a, hipStream_t s);
+// t2h_qk.hip
+hipError_t launch_qk(const QkArgs& a, const RopeSlots& tab, hipStream_t s);
+hipError_t launch_phases(const PhaseArgs& a, const RopeSlots& tab, hipStream_t s);
+// t2h_eltwise.hip
+hipError_t launch_activation(const EltArgs& a, hipStream_t s);
+hipError_t launch_gate_residual(const EltArgs& a, hipStream_t s);
+hipError_t launch_modulate(const EltArgs& a, hipStream_t s);
+hipError_t launch_binop_rows(const EltArgs& a, hipStream_t s);
+hipError_t launch_timestep(const float* t, void* out, int64_t n, int32_t dim, int32_t dtype,
+                           const float* freqs_host, hipStream_t s);
+hipError_t launch_offsets(const int32_t* coords, int64_t rows, int32_t coord_cols, int32_t nbatch,
+                          int64_t* offsets, int64_t* first_bad, hipStream_t s);
+hipError_t launch_modulation_add(const float* mod, const float* modulation, float* m, int64_t n,
+                                 int64_t width, hipStream_t s);
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+}  // namespace t2h

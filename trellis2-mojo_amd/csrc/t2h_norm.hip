@@ -1,0 +1,244 @@
+// LayerNorm + adaLN epilogue over token rows, and the fused gated-residual
+// join + LayerNorm (one HBM pass for `x += gate*(h+bias); y = LN(x)*(1+scale)+shift`).
+//
+// Fast path: one wave64 per row, the row held in VGPRs (C = 64 * NCH * E with
+// E = 16 B of storage per lane, e.g. C = 1536: f32 NCH 6, f16/bf16 NCH 3), so
+// the two-pass mean/variance never re-reads HBM. Waves are persistent and
+// stride over rows; the per-batch parameter rows (shift/scale, gate) stay in
+// VGPRs until the row's batch changes. Reductions are DPP row sums plus four
+// readlanes. Every output element follows the reference's f32 rounding
+// sequence; only the order of the two row sums differs from the reference.
+//
+// Reference: modules/nn.mojo:314-369 (LayerNorm32), 660-689 (modulate),
+// sparse/transformer/modulated.mojo:60-65 (gathered modulate),
+// gpu/block.mojo:47-110 (ln_mod_rows, gate_add_bias_rows).
+#include "t2h_device.h"
+#include "t2h_internal.h"
+
+namespace t2h {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = 64 * kWavesPerBlock;
+
+// y = LN epilogue of one normalised value n (f32), in the reference's order.
+__device__ __forceinline__ float ln_epilogue(float xv, float mean, float inv, int mode, float pa, float pb) {
+    const float n = mul_rn(sub_rn(xv, mean), inv);            // (x - mean) * inv_std
+    if (mode == T2H_LN_MODULATE) return add_rn(mul_rn(n, add_rn(1.0f, pb)), pa);  // n*(1+scale)+shift
+    if (mode == T2H_LN_AFFINE) return add_rn(mul_rn(n, pa), pb);                  // n*w + b
+    return n;
+}
+
+template <typename T, int NCH, bool JOIN>
+__global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
+    constexpr int E = kPack<T>;
+    constexpr int C = 64 * NCH * E;
+    const int lane = lane_id();
+    const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* __restrict__ h = static_cast<const T*>(a.h);
+    T* __restrict__ xo = static_cast<T*>(a.x_out);
+    T* __restrict__ yo = static_cast<T*>(a.y_out);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    const int64_t pst = a.p_stride;
+    const int64_t gst = a.gate_stride;
+    const float inv_c = 1.0f / (float)C;
+    (void)inv_c;
+
+    float pa[NCH][E], pb[NCH][E];   // epilogue params of batch cur_p
+    float jb[NCH][E], jg[NCH][E];   // join bias (fixed) and gate of batch cur_g
+    int32_t cur_p = -1, cur_g = -1;
+    if (JOIN) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int col = (c * 64 + lane) * E;
+            if (a.bias) load_params<E>(a.bias + col, jb[c]);
+        }
+    }
+
+    for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6); r < a.rows; r += nwaves) {
+        const int64_t base = r * (int64_t)C;
+        float v[NCH][E];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
+
+        const int32_t b = (a.mode == T2H_LN_MODULATE || (JOIN && a.gate)) ? bm.batch_of(r) : 0;
+        if (JOIN) {
+            float hv[NCH][E];
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
+            if (a.gate && b != cur_g) {
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) load_params<E>(a.gate + b * gst + (c * 64 + lane) * E, jg[c]);
+                cur_g = b;
+            }
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) {
+                    float t = a.bias ? add_rn(hv[c][i], jb[c][i]) : hv[c][i];
+                    if (a.gate) t = mul_rn(t, jg[c][i]);
+                    v[c][i] = round_to<T>(add_rn(v[c][i], t));
+                }
+                store_elems<T, E, true>(xo + base + (c * 64 + lane) * E, v[c]);
+            }
+        }
+
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int i = 0; i < E; ++i) s += v[c][i];
+        const float mean = wave_sum(s) / (float)C;
+        float q = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float d = v[c][i] - mean;
+                q += d * d;
+            }
+        const float var = wave_sum(q) / (float)C;
+        const float inv = 1.0f / sqrtf(var + a.eps);
+
+        if (a.mode != T2H_LN_PLAIN) {
+            const int32_t pbx = (a.mode == T2H_LN_MODULATE) ? b : 0;
+            if (pbx != cur_p) {
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const int col = (c * 64 + lane) * E;
+                    load_params<E>(a.p0 + pbx * pst + col, pa[c]);
+                    load_params<E>(a.p1 + pbx * pst + col, pb[c]);
+                }
+                cur_p = pbx;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            float y[E];
+#pragma unroll
+            for (int i = 0; i < E; ++i)
+                y[i] = ln_epilogue(v[c][i], mean, inv, a.mode,
+                                   a.mode != T2H_LN_PLAIN ? pa[c][i] : 0.0f,
+                                   a.mode != T2H_LN_PLAIN ? pb[c][i] : 0.0f);
+            store_elems<T, E, true>(yo + base + (c * 64 + lane) * E, y);
+        }
+    }
+}
+
+// Any cols: one 256-thread block per row (grid-stride), block reduction
+// through LDS, values re-read from memory for each pass.
+template <typename T, bool JOIN>
+__global__ __launch_bounds__(kBlock) void ln_rows_generic(LnArgs a) {
+    __shared__ float red[kWavesPerBlock];
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* __restrict__ h = static_cast<const T*>(a.h);
+    T* __restrict__ xo = static_cast<T*>(a.x_out);
+    T* __restrict__ yo = static_cast<T*>(a.y_out);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    const int C = a.cols;
+    const int tid = threadIdx.x, wid = tid >> 6;
+
+    auto block_sum = [&](float v) -> float {
+        v = wave_sum(v);
+        __syncthreads();
+        if ((tid & 63) == 0) red[wid] = v;
+        __syncthreads();
+        return (red[0] + red[1]) + (red[2] + red[3]);
+    };
+
+    for (int64_t r = blockIdx.x; r < a.rows; r += gridDim.x) {
+        const int64_t base = r * (int64_t)C;
+        const int32_t b = (a.mode == T2H_LN_MODULATE || (JOIN && a.gate)) ? bm.batch_of(r) : 0;
+        auto value = [&](int c) -> float {
+            float xv = ld1(x + base + c);
+            if (JOIN) {
+                float t = ld1(h + base + c);
+                if (a.bias) t = add_rn(t, a.bias[c]);
+                if (a.gate) t = mul_rn(t, a.gate[b * a.gate_stride + c]);
+                xv = round_to<T>(add_rn(xv, t));
+            }
+            return xv;
+        };
+        float s = 0.0f;
+        for (int c = tid; c < C; c += kBlock) {
+            const float xv = value(c);
+            if (JOIN) st1(xo + base + c, xv);
+            s += xv;
+        }
+        const float mean = block_sum(s) / (float)C;
+        float q = 0.0f;
+        for (int c = tid; c < C; c += kBlock) {
+            const float d = value(c) - mean;
+            q += d * d;
+        }
+        const float var = block_sum(q) / (float)C;
+        const float inv = 1.0f / sqrtf(var + a.eps);
+        const int32_t pbx = (a.mode == T2H_LN_MODULATE) ? b : 0;
+        for (int c = tid; c < C; c += kBlock) {
+            const float pa = a.mode != T2H_LN_PLAIN ? a.p0[pbx * a.p_stride + c] : 0.0f;
+            const float pb = a.mode != T2H_LN_PLAIN ? a.p1[pbx * a.p_stride + c] : 0.0f;
+            st1(yo + base + c, ln_epilogue(value(c), mean, inv, a.mode, pa, pb));
+        }
+    }
+}
+
+template <typename K>
+int resident_blocks(K kernel) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, kBlock, 0) != hipSuccess || nb <= 0) nb = 2;
+    return nb * device_cu_count();
+}
+
+template <typename T, int NCH, bool JOIN>
+hipError_t launch_fast(const LnArgs& a, hipStream_t s) {
+    auto k = ln_rows_kernel<T, NCH, JOIN>;
+    static const int cap = resident_blocks(k);
+    const int64_t need = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int grid = (int)(need < cap ? need : cap);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T, bool JOIN>
+hipError_t launch_typed(const LnArgs& a, hipStream_t s) {
+    constexpr int E = kPack<T>;
+    const bool aligned = al16(a.x) && al16(a.h) && al16(a.x_out) && al16(a.y_out) && al16(a.p0) &&
+                         al16(a.p1) && al16(a.bias) && al16(a.gate) && (a.p_stride % 4 == 0) &&
+                         (a.gate_stride % 4 == 0);
+    if (aligned && a.cols % (64 * E) == 0) {
+        switch (a.cols / (64 * E)) {
+            case 1: return launch_fast<T, 1, JOIN>(a, s);
+            case 2: return launch_fast<T, 2, JOIN>(a, s);
+            case 3: return launch_fast<T, 3, JOIN>(a, s);
+            case 4: return launch_fast<T, 4, JOIN>(a, s);
+            case 6: return launch_fast<T, 6, JOIN>(a, s);
+            case 8: return launch_fast<T, 8, JOIN>(a, s);
+            default: break;
+        }
+    }
+    auto k = ln_rows_generic<T, JOIN>;
+    static const int cap = resident_blocks(k);
+    const int grid = (int)(a.rows < cap ? a.rows : cap);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+template <bool JOIN>
+hipError_t launch_join(const LnArgs& a, hipStream_t s) {
+    switch (a.dtype) {
+        case T2H_F32: return launch_typed<float, JOIN>(a, s);
+        case T2H_F16: return launch_typed<_Float16, JOIN>(a, s);
+        default: return launch_typed<__bf16, JOIN>(a, s);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_ln(const LnArgs& a, hipStream_t s) {
+    return a.h ? launch_join<true>(a, s) : launch_join<false>(a, s);
+}
+
+}  // namespace t2h

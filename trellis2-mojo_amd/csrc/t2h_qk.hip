@@ -1,0 +1,349 @@
+// Multi-head QK RMSNorm + 3D RoPE (+ qkv bias) on token rows, and the RoPE
+// phase-table builder.
+//
+// Fast path (head_dim 64 or 128, heads <= 16): one wave64 per token row.
+// Each head is handled by one DPP row of 16 lanes (lane m holds elements
+// [m*E, m*E+E), E = head_dim/16), so a wave instruction covers 4 heads and the
+// per-head sum of squares is a 4-step DPP row sum with no LDS. The interleaved
+// RoPE pairs (2p, 2p+1) are lane-local. Each lane computes cos/sin of its E/2
+// slots once per row from the row's integer voxel coordinates (or the dense
+// grid index, or a precomputed phase table) and reuses them for every head of
+// q and k, so no phase table is read from HBM. Waves are persistent and keep
+// gamma_q/gamma_k in VGPRs across rows.
+//
+// Reference: sparse/attention/modules.mojo:37-102 (MultiHeadRMSNorm),
+// modules/rope.mojo:17-88, sparse/attention/rope.mojo:20-134 (RoPE),
+// gpu/attention.mojo:507-563 (bias_rms_rope_qkv), 596-631 (bias_rms_q).
+#include "t2h_device.h"
+#include "t2h_internal.h"
+
+namespace t2h {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+
+// Position of token row r along `axis` (f32, exact for |coord| < 2^24).
+struct PosSource {
+    const int32_t* coords;
+    int32_t coord_cols;
+    int32_t grid_res;
+    int32_t pos_dim;
+    __device__ __forceinline__ void get(int64_t r, float* pos) const {
+        if (coords != nullptr) {
+            const int32_t* cr = coords + r * (int64_t)coord_cols + 1;
+#pragma unroll
+            for (int ax = 0; ax < T2H_MAX_POS_DIM; ++ax) pos[ax] = ax < pos_dim ? (float)cr[ax] : 0.0f;
+        } else {
+            const int64_t R = grid_res;
+            const int64_t l = r % (R * R * R);
+            pos[0] = (float)(l / (R * R));
+            pos[1] = (float)((l / R) % R);
+            pos[2] = (float)(l % R);
+            pos[3] = 0.0f;
+        }
+    }
+};
+
+__device__ __forceinline__ float pick_axis(const float* pos, int ax) {
+    return ax == 0 ? pos[0] : ax == 1 ? pos[1] : ax == 2 ? pos[2] : pos[3];
+}
+
+// cos/sin of one slot: angle = pos[axis] * freq rounded to f32, then accurate
+// (full-range reduced) cosf/sinf; identity for pad slots (axis < 0).
+__device__ __forceinline__ void slot_phase(const float* pos, int ax, float freq, float& c, float& s) {
+    if (ax < 0) {
+        c = 1.0f;
+        s = 0.0f;
+    } else {
+        const float angle = __fmul_rn(pick_axis(pos, ax), freq);
+        sincosf(angle, &s, &c);
+    }
+}
+
+template <typename T, int D, int NG>
+__global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab) {
+    constexpr int E = D / 16;   // elements per lane per head
+    constexpr int P = E / 2;    // rotary slots per lane
+    const int lane = lane_id();
+    const int g = lane >> 4;
+    const int m = lane & 15;
+    const int H = a.heads;
+    const int64_t HD = (int64_t)H * D;
+    const T* __restrict__ qi = static_cast<const T*>(a.q_in);
+    const T* __restrict__ ki = static_cast<const T*>(a.k_in);
+    T* __restrict__ qo = static_cast<T*>(a.q_out);
+    T* __restrict__ ko = static_cast<T*>(a.k_out);
+    const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
+    const bool rms = a.gamma_q != nullptr || a.gamma_k != nullptr;
+    const float sc = a.rms_scale;
+
+    // lane-constant slot table and gammas
+    float sf[P];
+    int sa[P];
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+        sf[t] = tab.freq[m * P + t];
+        sa[t] = tab.axis[m * P + t];
+    }
+    float gq[NG][E], gk[NG][E];
+#pragma unroll
+    for (int it = 0; it < NG; ++it) {
+        const int hh = 4 * it + g;
+        const int64_t off = (int64_t)hh * D + m * E;
+#pragma unroll
+        for (int i = 0; i < E; ++i) { gq[it][i] = 1.0f; gk[it][i] = 1.0f; }
+        if (hh < H) {
+            if (a.gamma_q) load_params<E>(a.gamma_q + off, gq[it]);
+            if (a.gamma_k) load_params<E>(a.gamma_k + off, gk[it]);
+        }
+    }
+
+    const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+    for (int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); r < a.rows; r += nwaves) {
+        float qv[NG][E], kv[NG][E];
+#pragma unroll
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+            const int64_t off = r * a.in_stride + (int64_t)hh * D + m * E;
+#pragma unroll
+            for (int i = 0; i < E; ++i) { qv[it][i] = 0.0f; kv[it][i] = 0.0f; }
+            if (hh < H) {
+                if (qi) load_elems<T, E, true>(qi + off, qv[it]);
+                if (ki) load_elems<T, E, true>(ki + off, kv[it]);
+            }
+        }
+
+        float pc[P], ps[P];
+        if (a.use_rope) {
+            if (a.phases != nullptr) {
+                const int64_t l = r % a.phase_rows;
+                float tmp[2 * P];  // P interleaved (cos, sin) pairs
+                load_params<2 * P>(a.phases + (l * (D / 2) + m * P) * 2, tmp);
+#pragma unroll
+                for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
+            } else {
+                float pos[T2H_MAX_POS_DIM];
+                src.get(r, pos);
+#pragma unroll
+                for (int t = 0; t < P; ++t) slot_phase(pos, sa[t], sf[t], pc[t], ps[t]);
+            }
+        }
+
+        auto process = [&](float (&v)[NG][E], const float (&gm)[NG][E], const float* bias,
+                           bool has_gamma, T* __restrict__ out) {
+#pragma unroll
+            for (int it = 0; it < NG; ++it) {
+                const int hh = 4 * it + g;
+                const bool valid = hh < H;
+                if (bias != nullptr && valid) {
+                    float bv[E];
+                    load_params<E>(bias + (int64_t)hh * D + m * E, bv);
+#pragma unroll
+                    for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
+                }
+                if (has_gamma) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < E; ++i) ss += v[it][i] * v[it][i];
+                    ss = row16_sum(ss);
+                    float nrm = sqrtf(ss);
+                    if (nrm < 1e-12f) nrm = 1e-12f;
+                    const float rn = 1.0f / nrm;
+#pragma unroll
+                    for (int i = 0; i < E; ++i) v[it][i] = v[it][i] * rn * gm[it][i] * sc;
+                }
+                if (a.use_rope) {
+#pragma unroll
+                    for (int t = 0; t < P; ++t) {
+                        const float re = v[it][2 * t], im = v[it][2 * t + 1];
+                        v[it][2 * t] = re * pc[t] - im * ps[t];
+                        v[it][2 * t + 1] = re * ps[t] + im * pc[t];
+                    }
+                }
+                if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
+            }
+        };
+        if (qi) process(qv, gq, a.bias_q, rms && a.gamma_q != nullptr, qo);
+        if (ki) process(kv, gk, a.bias_k, rms && a.gamma_k != nullptr, ko);
+
+        if (a.v != nullptr && a.bias_v != nullptr) {  // packed qkv: v += bias_v
+            T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
+            for (int64_t e0 = (int64_t)lane * E; e0 < HD; e0 += 64 * E) {
+                float vv[E], bv[E];
+                load_elems<T, E>(vr + e0, vv);
+                load_params<E>(a.bias_v + e0, bv);
+#pragma unroll
+                for (int i = 0; i < E; ++i) vv[i] = add_rn(vv[i], bv[i]);
+                store_elems<T, E>(vr + e0, vv);
+            }
+        }
+    }
+}
+
+// Any even head_dim / any head count: one wave per (row, head); lanes stride
+// over the pairs of the head.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void qk_rows_generic(QkArgs a, RopeSlots tab) {
+    const int lane = lane_id();
+    const int D = a.head_dim, half = D / 2, H = a.heads;
+    const T* __restrict__ qi = static_cast<const T*>(a.q_in);
+    const T* __restrict__ ki = static_cast<const T*>(a.k_in);
+    T* __restrict__ qo = static_cast<T*>(a.q_out);
+    T* __restrict__ ko = static_cast<T*>(a.k_out);
+    const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
+    const int64_t units = a.rows * H;
+    const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+    for (int64_t u = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); u < units; u += nwaves) {
+        const int64_t r = u / H;
+        const int hh = (int)(u % H);
+        float pos[T2H_MAX_POS_DIM];
+        if (a.use_rope && a.phases == nullptr) src.get(r, pos);
+        for (int which = 0; which < 2; ++which) {
+            const T* in = which == 0 ? qi : ki;
+            if (in == nullptr) continue;
+            T* out = which == 0 ? qo : ko;
+            const float* bias = which == 0 ? a.bias_q : a.bias_k;
+            const float* gm = which == 0 ? a.gamma_q : a.gamma_k;
+            const int64_t ib = r * a.in_stride + (int64_t)hh * D;
+            const int64_t ob = r * a.out_stride + (int64_t)hh * D;
+            float ss = 0.0f;
+            for (int p = lane; p < half; p += 64) {
+                float re = ld1(in + ib + 2 * p), im = ld1(in + ib + 2 * p + 1);
+                if (bias) { re = add_rn(re, bias[hh * D + 2 * p]); im = add_rn(im, bias[hh * D + 2 * p + 1]); }
+                ss += re * re + im * im;
+            }
+            float rn = 1.0f;
+            if (gm != nullptr) {
+                ss = wave_sum(ss);
+                float nrm = sqrtf(ss);
+                if (nrm < 1e-12f) nrm = 1e-12f;
+                rn = 1.0f / nrm;
+            }
+            for (int p = lane; p < half; p += 64) {
+                float re = ld1(in + ib + 2 * p), im = ld1(in + ib + 2 * p + 1);
+                if (bias) { re = add_rn(re, bias[hh * D + 2 * p]); im = add_rn(im, bias[hh * D + 2 * p + 1]); }
+                if (gm != nullptr) {
+                    re = re * rn * gm[hh * D + 2 * p] * a.rms_scale;
+                    im = im * rn * gm[hh * D + 2 * p + 1] * a.rms_scale;
+                }
+                if (a.use_rope) {
+                    float c, s;
+                    if (a.phases != nullptr) {
+                        const int64_t l = r % a.phase_rows;
+                        c = a.phases[(l * half + p) * 2];
+                        s = a.phases[(l * half + p) * 2 + 1];
+                    } else {
+                        slot_phase(pos, tab.axis[p], tab.freq[p], c, s);
+                    }
+                    const float nre = re * c - im * s;
+                    const float nim = re * s + im * c;
+                    re = nre;
+                    im = nim;
+                }
+                st1(out + ob + 2 * p, re);
+                st1(out + ob + 2 * p + 1, im);
+            }
+        }
+        if (a.v != nullptr && a.bias_v != nullptr) {
+            T* vr = static_cast<T*>(a.v) + r * a.in_stride + (int64_t)hh * D;
+            for (int e = lane; e < D; e += 64) st1(vr + e, add_rn(ld1(vr + e), a.bias_v[hh * D + e]));
+        }
+    }
+}
+
+// Phase table [rows, D/2, 2]: one thread per (row, slot).
+__global__ __launch_bounds__(kBlock) void phases_kernel(PhaseArgs a, RopeSlots tab) {
+    const int half = a.head_dim / 2;
+    const int64_t total = a.rows * half;
+    const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (int64_t)gridDim.x * kBlock) {
+        const int64_t r = i / half;
+        const int p = (int)(i % half);
+        float pos[T2H_MAX_POS_DIM];
+        if (a.positions != nullptr) {
+#pragma unroll
+            for (int ax = 0; ax < T2H_MAX_POS_DIM; ++ax)
+                pos[ax] = ax < a.pos_dim ? a.positions[r * a.pos_dim + ax] : 0.0f;
+        } else {
+            src.get(r, pos);
+        }
+        float c, s;
+        slot_phase(pos, tab.axis[p], tab.freq[p], c, s);
+        reinterpret_cast<float2*>(a.out)[i] = make_float2(c, s);
+    }
+}
+
+template <typename K>
+int resident_blocks(K kernel) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, kBlock, 0) != hipSuccess || nb <= 0) nb = 2;
+    return nb * device_cu_count();
+}
+
+template <typename T, int D, int NG>
+hipError_t launch_fast(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
+    auto k = qk_rows_kernel<T, D, NG>;
+    static const int cap = resident_blocks(k);
+    const int64_t need = (a.rows + kWaves - 1) / kWaves;
+    const int grid = (int)(need < cap ? need : cap);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a, tab);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_d(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
+    switch ((a.heads + 3) / 4) {
+        case 1: return launch_fast<T, D, 1>(a, tab, s);
+        case 2: return launch_fast<T, D, 2>(a, tab, s);
+        case 3: return launch_fast<T, D, 3>(a, tab, s);
+        default: return launch_fast<T, D, 4>(a, tab, s);
+    }
+}
+
+inline bool aligned_to(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+template <typename T>
+hipError_t launch_typed(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
+    // vector loads of min(16, E * sizeof(T)) bytes per lane need that alignment
+    const int E = a.head_dim / 16;
+    const int chunk = E * (int)sizeof(T) < 16 ? E * (int)sizeof(T) : 16;
+    const int64_t ealign = chunk / (int64_t)sizeof(T);
+    const bool aligned = (a.in_stride % ealign == 0) && (a.out_stride % ealign == 0) &&
+                         aligned_to(a.q_in, chunk) && aligned_to(a.k_in, chunk) &&
+                         aligned_to(a.q_out, chunk) && aligned_to(a.k_out, chunk) &&
+                         aligned_to(a.v, chunk) && aligned_to(a.bias_q, 16) && aligned_to(a.bias_k, 16) &&
+                         aligned_to(a.bias_v, 16) && aligned_to(a.gamma_q, 16) &&
+                         aligned_to(a.gamma_k, 16) && aligned_to(a.phases, 16);
+    if (a.heads <= 16 && aligned) {
+        if (a.head_dim == 128) return launch_d<T, 128>(a, tab, s);
+        if (a.head_dim == 64) return launch_d<T, 64>(a, tab, s);
+    }
+    auto k = qk_rows_generic<T>;
+    static const int cap = resident_blocks(k);
+    const int64_t need = (a.rows * a.heads + kWaves - 1) / kWaves;
+    const int grid = (int)(need < cap ? need : cap);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a, tab);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_qk(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
+    switch (a.dtype) {
+        case T2H_F32: return launch_typed<float>(a, tab, s);
+        case T2H_F16: return launch_typed<_Float16>(a, tab, s);
+        default: return launch_typed<__bf16>(a, tab, s);
+    }
+}
+
+hipError_t launch_phases(const PhaseArgs& a, const RopeSlots& tab, hipStream_t s) {
+    const int64_t total = a.rows * (a.head_dim / 2);
+    int64_t grid = (total + kBlock - 1) / kBlock;
+    const int64_t cap = 64LL * device_cu_count();
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(phases_kernel, dim3((unsigned)grid), dim3(kBlock), 0, s, a, tab);
+    return hipGetLastError();
+}
+
+}  // namespace t2h
