@@ -94,6 +94,7 @@ class Chain:
             "qk_rmsnorm_rope": 4 * T * C * e + T * 16 + 2 * H * D * 4,
             "gelu_tanh_bias": 2 * T * F * e + F * 4,
             "gate_residual": 3 * T * C * e + C * 4,
+            "copy": 2 * T * F * e,
         }
         self.chain_bytes = (6144 + 12304 + 24576 + 9216) * T   # BASELINE.md byte model
 
@@ -111,6 +112,10 @@ class Chain:
             return lambda: o.activation(self.u, o.ACT_GELU_TANH, bias=self.bias, out=self.gout)
         if name == "gate_residual":
             return lambda: o.gate_residual(self.x, self.y, gate=self.gate, offsets=self.offsets, out=self.res)
+        if name == "copy":  # calibration: a plain device copy of the GELU tensor (torch's copy kernel)
+            return lambda: self.gout.copy_(self.u)
+        if name == "chain":
+            return self.step
         raise KeyError(name)
 
     ORDER = ["timestep", "ln_modulate", "qk_rmsnorm_rope", "gelu_tanh_bias", "gate_residual"]
@@ -261,12 +266,13 @@ def main():
     chain = Chain(dev, dtype)
     log(f"config5: T={chain.T} tokens, chain bytes {chain.chain_bytes/1e9:.3f} GB/step")
 
-    if args.op:
+    if args.op:  # one op (or "chain") only, for profiler runs
         fn = chain.op(args.op)
         for _ in range(args.warmup):
             fn()
         ms = time_region(torch, fn, args.steps)
-        log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {chain.bytes[args.op]/(ms/args.steps)/1e6:.1f} GB/s")
+        nb = chain.chain_bytes if args.op == "chain" else chain.bytes[args.op]
+        log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {nb/(ms/args.steps)/1e6:.1f} GB/s")
         return
 
     for _ in range(args.warmup):

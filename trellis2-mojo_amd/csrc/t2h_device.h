@@ -71,11 +71,16 @@ template <> struct Word<__bf16> {
     }
 };
 
+#ifndef T2H_NT
+#define T2H_NT 1
+#endif
+
 // Load / store E contiguous elements of T as f32 (E * sizeof(T) is a multiple
 // of 8 bytes; 16-byte pieces where possible). NT = non-temporal hint for data
 // that is streamed once.
-template <typename T, int E, bool NT = false>
+template <typename T, int E, bool NT_ = false>
 __device__ __forceinline__ void load_elems(const T* __restrict__ p, float* f) {
+    constexpr bool NT = NT_ && T2H_NT;
     constexpr int BYTES = E * (int)sizeof(T);
     static_assert(BYTES % 8 == 0, "vector width");
     constexpr int WN = Word<T>::N;
@@ -100,8 +105,9 @@ __device__ __forceinline__ void load_elems(const T* __restrict__ p, float* f) {
     }
 }
 
-template <typename T, int E, bool NT = false>
+template <typename T, int E, bool NT_ = false>
 __device__ __forceinline__ void store_elems(T* __restrict__ p, const float* f) {
+    constexpr bool NT = NT_ && T2H_NT;
     constexpr int BYTES = E * (int)sizeof(T);
     static_assert(BYTES % 8 == 0, "vector width");
     constexpr int WN = Word<T>::N;
@@ -164,10 +170,22 @@ template <> __device__ __forceinline__ float round_to<__bf16>(float v) {
 
 // Explicit IEEE single roundings, never contracted into an FMA: the
 // bit-exact paths (modulate, gated residual, binop) use these so that
-// a*b+c stays two roundings as in the reference.
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+// a*b+c stays two roundings as in the reference. HIP compiles with
+// -ffp-contract=fast (and __fmul_rn/__fadd_rn are plain * and +), so the
+// operations are emitted without the `contract` flag, which stops the
+// backend from fusing them with a neighbouring add/mul after inlining.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
 
 // ---------------------------------------------------------------------------
 // DPP reductions (gfx9 DPP controls; all lanes of a row must be active)

@@ -2,8 +2,8 @@
 // batch-broadcast binop, sinusoidal timestep embedding, coords -> batch
 // offsets, share_mod modulation add.
 //
-// Row-tiled layout: a 256-thread block covers 256 * V columns (V = 16 B of
-// storage per thread) of RPT consecutive rows. Per-column parameters (bias)
+// Row-tiled layout: a block covers RPT consecutive rows and blockDim * V
+// columns (V = 16 B of storage per thread; one whole row when it fits). Per-column parameters (bias)
 // are loaded once per thread; per-batch parameter rows (gate, shift/scale,
 // `other`) are reloaded only when the tile's row crosses a batch boundary
 // (the batch of a row is block-uniform). All RPT rows are loaded before any
@@ -23,7 +23,10 @@ namespace t2h {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kRpt = 4;  // rows per thread
+#ifndef T2H_ELT_RPT
+#define T2H_ELT_RPT 4
+#endif
+constexpr int kRpt = T2H_ELT_RPT;  // rows per thread
 
 // ---- activations (f32 math) ------------------------------------------------
 // GELU-tanh: 0.5*v*(1+tanh(z)) == v * sigmoid(2z) == v / (1 + exp(-2z)), with
@@ -78,24 +81,37 @@ struct Tile {
     int nrows;
 };
 
+// Tile of this block, 1-D grid. When a row is a whole number of waves of
+// 16-byte vectors (cols / V = blockDim.x <= 1024), a block is exactly one row
+// wide and covers kRpt full rows: every thread is busy and the block streams
+// one contiguous span. Otherwise blocks are kBlock * V columns wide and
+// consecutive blocks walk the column tiles of a row tile first, so blocks
+// that run together still stream contiguous rows.
 template <int V>
 __device__ __forceinline__ bool tile_of(const EltArgs& a, Tile& t) {
-    t.col0 = ((int64_t)blockIdx.y * kBlock + threadIdx.x) * V;
-    t.r0 = (int64_t)blockIdx.x * kRpt;
+    const int64_t bw = (int64_t)blockDim.x * V;   // columns per block
+    const int64_t ct = (a.cols + bw - 1) / bw;
+    const int64_t rt = ct == 1 ? (int64_t)blockIdx.x : (int64_t)blockIdx.x / ct;
+    t.col0 = (((int64_t)blockIdx.x - rt * ct) * blockDim.x + threadIdx.x) * V;
+    t.r0 = rt * kRpt;
     const int64_t left = a.rows - t.r0;
     t.nrows = left < kRpt ? (int)left : kRpt;
     return t.col0 < a.cols;
 }
 
 // ---- activation(x + bias) ----------------------------------------------------
-template <typename T, int V, int KIND>
-__global__ __launch_bounds__(kBlock) void act_kernel(EltArgs a) {
+// x + b as fma(x, 1, b): one rounding of the exact sum, i.e. the same bits as
+// the reference's `acc += b`, in a form that fuses with the f16 -> f32 convert.
+__device__ __forceinline__ float bias_add(float x, float b) { return __builtin_fmaf(x, 1.0f, b); }
+
+template <typename T, int V, int KIND, bool BIAS>
+__global__ __launch_bounds__(1024) void act_kernel(EltArgs a) {
     Tile t;
     if (!tile_of<V>(a, t)) return;
     const T* __restrict__ x = static_cast<const T*>(a.x);
     T* __restrict__ o = static_cast<T*>(a.out);
     float bias[V];
-    if (a.bias) ldp<V>(a.bias + t.col0, bias);
+    if (BIAS) ldp<V>(a.bias + t.col0, bias);
     float v[kRpt][V];
 #pragma unroll
     for (int k = 0; k < kRpt; ++k)
@@ -104,17 +120,14 @@ __global__ __launch_bounds__(kBlock) void act_kernel(EltArgs a) {
     for (int k = 0; k < kRpt; ++k) {
         if (k >= t.nrows) break;
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-            const float u = a.bias ? add_rn(v[k][i], bias[i]) : v[k][i];   // linear bias: acc + b
-            v[k][i] = act_f<KIND>(u);
-        }
+        for (int i = 0; i < V; ++i) v[k][i] = act_f<KIND>(BIAS ? bias_add(v[k][i], bias[i]) : v[k][i]);
         st<T, V>(o + (t.r0 + k) * a.cols + t.col0, v[k]);
     }
 }
 
 // ---- out = x + fl(fl(h + bias) * gate[b]) ------------------------------------
 template <typename T, int V>
-__global__ __launch_bounds__(kBlock) void gate_res_kernel(EltArgs a) {
+__global__ __launch_bounds__(1024) void gate_res_kernel(EltArgs a) {
     Tile t;
     if (!tile_of<V>(a, t)) return;
     const T* __restrict__ x = static_cast<const T*>(a.x);
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(kBlock) void gate_res_kernel(EltArgs a) {
 
 // ---- out = fl(fl(x * fl(1 + scale[b])) + shift[b]) ---------------------------
 template <typename T, int V>
-__global__ __launch_bounds__(kBlock) void modulate_kernel(EltArgs a) {
+__global__ __launch_bounds__(1024) void modulate_kernel(EltArgs a) {
     Tile t;
     if (!tile_of<V>(a, t)) return;
     const T* __restrict__ x = static_cast<const T*>(a.x);
@@ -194,7 +207,7 @@ __device__ __forceinline__ float apply_op(float x, float y, int op) {
 }
 
 template <typename T, int V>
-__global__ __launch_bounds__(kBlock) void binop_kernel(EltArgs a) {
+__global__ __launch_bounds__(1024) void binop_kernel(EltArgs a) {
     Tile t;
     if (!tile_of<V>(a, t)) return;
     const T* __restrict__ x = static_cast<const T*>(a.x);
@@ -305,15 +318,21 @@ bool vec_ok(const EltArgs& a) {
            al16(a.shift) && a.p_stride % 4 == 0;
 }
 
+// Block width in threads: one row of 16-byte vectors when that is a whole
+// number of waves (<= 1024 threads), else kBlock.
 template <int V>
-dim3 tile_grid(const EltArgs& a) {
-    const int64_t rt = (a.rows + kRpt - 1) / kRpt;
-    const int64_t ct = (a.cols + (int64_t)kBlock * V - 1) / ((int64_t)kBlock * V);
-    return dim3((unsigned)rt, (unsigned)ct);
+int tile_block(const EltArgs& a) {
+    if (V > 1 && a.cols % (64 * V) == 0 && a.cols / V <= 1024) return a.cols / V;
+    return kBlock;
 }
 
-template <template <typename, int> class K, typename T>
-struct Unused {};
+template <int V>
+dim3 tile_grid(const EltArgs& a) {
+    const int64_t bw = (int64_t)tile_block<V>(a) * V;
+    const int64_t rt = (a.rows + kRpt - 1) / kRpt;
+    const int64_t ct = (a.cols + bw - 1) / bw;
+    return dim3((unsigned)(rt * ct));
+}
 
 #define T2H_DISPATCH_DTYPE(DT, FN, ...)                                \
     switch (DT) {                                                      \
@@ -322,14 +341,19 @@ struct Unused {};
         default: return FN<__bf16>(__VA_ARGS__);                       \
     }
 
-template <typename T, int KIND>
-hipError_t act_typed_kind(const EltArgs& a, hipStream_t s) {
+template <typename T, int KIND, bool BIAS>
+hipError_t act_launch(const EltArgs& a, hipStream_t s) {
     constexpr int V = kPack<T>;
     if (vec_ok<T>(a))
-        hipLaunchKernelGGL((act_kernel<T, V, KIND>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((act_kernel<T, V, KIND, BIAS>), tile_grid<V>(a), dim3(tile_block<V>(a)), 0, s, a);
     else
-        hipLaunchKernelGGL((act_kernel<T, 1, KIND>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((act_kernel<T, 1, KIND, BIAS>), tile_grid<1>(a), dim3(tile_block<1>(a)), 0, s, a);
     return hipGetLastError();
+}
+
+template <typename T, int KIND>
+hipError_t act_typed_kind(const EltArgs& a, hipStream_t s) {
+    return a.bias ? act_launch<T, KIND, true>(a, s) : act_launch<T, KIND, false>(a, s);
 }
 
 template <typename T>
@@ -346,9 +370,9 @@ template <typename T>
 hipError_t gate_res_typed(const EltArgs& a, hipStream_t s) {
     constexpr int V = kPack<T>;
     if (vec_ok<T>(a))
-        hipLaunchKernelGGL((gate_res_kernel<T, V>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((gate_res_kernel<T, V>), tile_grid<V>(a), dim3(tile_block<V>(a)), 0, s, a);
     else
-        hipLaunchKernelGGL((gate_res_kernel<T, 1>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((gate_res_kernel<T, 1>), tile_grid<1>(a), dim3(tile_block<1>(a)), 0, s, a);
     return hipGetLastError();
 }
 
@@ -356,9 +380,9 @@ template <typename T>
 hipError_t modulate_typed(const EltArgs& a, hipStream_t s) {
     constexpr int V = kPack<T>;
     if (vec_ok<T>(a))
-        hipLaunchKernelGGL((modulate_kernel<T, V>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((modulate_kernel<T, V>), tile_grid<V>(a), dim3(tile_block<V>(a)), 0, s, a);
     else
-        hipLaunchKernelGGL((modulate_kernel<T, 1>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((modulate_kernel<T, 1>), tile_grid<1>(a), dim3(tile_block<1>(a)), 0, s, a);
     return hipGetLastError();
 }
 
@@ -366,9 +390,9 @@ template <typename T>
 hipError_t binop_typed(const EltArgs& a, hipStream_t s) {
     constexpr int V = kPack<T>;
     if (vec_ok<T>(a))
-        hipLaunchKernelGGL((binop_kernel<T, V>), tile_grid<V>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((binop_kernel<T, V>), tile_grid<V>(a), dim3(tile_block<V>(a)), 0, s, a);
     else
-        hipLaunchKernelGGL((binop_kernel<T, 1>), tile_grid<1>(a), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((binop_kernel<T, 1>), tile_grid<1>(a), dim3(tile_block<1>(a)), 0, s, a);
     return hipGetLastError();
 }
 

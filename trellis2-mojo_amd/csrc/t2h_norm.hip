@@ -18,18 +18,26 @@
 namespace t2h {
 namespace {
 
+#ifndef T2H_LN_RPW
+#define T2H_LN_RPW 2
+#endif
+#ifndef T2H_LN_PERSIST
+#define T2H_LN_PERSIST 1
+#endif
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = 64 * kWavesPerBlock;
 
-// y = LN epilogue of one normalised value n (f32), in the reference's order.
-__device__ __forceinline__ float ln_epilogue(float xv, float mean, float inv, int mode, float pa, float pb) {
-    const float n = mul_rn(sub_rn(xv, mean), inv);            // (x - mean) * inv_std
-    if (mode == T2H_LN_MODULATE) return add_rn(mul_rn(n, add_rn(1.0f, pb)), pa);  // n*(1+scale)+shift
-    if (mode == T2H_LN_AFFINE) return add_rn(mul_rn(n, pa), pb);                  // n*w + b
+// y = LN epilogue of one centred value d = x - mean (f32), in the reference's
+// order: n = d * inv_std, then n * (1 + scale) + shift (pb holds the already
+// rounded 1 + scale) or n * w + b.
+__device__ __forceinline__ float ln_epilogue(float d, float inv, int mode, float pa, float pb) {
+    const float n = mul_rn(d, inv);
+    if (mode == T2H_LN_MODULATE) return add_rn(mul_rn(n, pb), pa);
+    if (mode == T2H_LN_AFFINE) return add_rn(mul_rn(n, pa), pb);
     return n;
 }
 
-template <typename T, int NCH, bool JOIN>
+template <typename T, int NCH, bool JOIN, int RPW>
 __global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
     constexpr int E = kPack<T>;
     constexpr int C = 64 * NCH * E;
@@ -42,86 +50,99 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
     const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
     const int64_t pst = a.p_stride;
     const int64_t gst = a.gate_stride;
-    const float inv_c = 1.0f / (float)C;
-    (void)inv_c;
+    const bool need_b = a.mode == T2H_LN_MODULATE || (JOIN && a.gate);
 
     float pa[NCH][E], pb[NCH][E];   // epilogue params of batch cur_p
     float jb[NCH][E], jg[NCH][E];   // join bias (fixed) and gate of batch cur_g
     int32_t cur_p = -1, cur_g = -1;
-    if (JOIN) {
+    if (JOIN && a.bias) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int col = (c * 64 + lane) * E;
-            if (a.bias) load_params<E>(a.bias + col, jb[c]);
-        }
+        for (int c = 0; c < NCH; ++c) load_params<E>(a.bias + (c * 64 + lane) * E, jb[c]);
     }
 
-    for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6); r < a.rows; r += nwaves) {
-        const int64_t base = r * (int64_t)C;
-        float v[NCH][E];
+    // RPW consecutive rows per wave per iteration: all their loads are issued
+    // before any reduction, so each wave keeps RPW rows in flight.
+    const int64_t wave = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    for (int64_t r0 = wave * RPW; r0 < a.rows; r0 += nwaves * RPW) {
+        float v[RPW][NCH][E];
+        float hv[RPW][NCH][E];
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
+        for (int k = 0; k < RPW; ++k) {
+            if (r0 + k < a.rows) {
+                const int64_t base = (r0 + k) * (int64_t)C;
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[k][c]);
+                    if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[k][c]);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int64_t r = r0 + k;
+            if (r >= a.rows) break;
+            const int64_t base = r * (int64_t)C;
+            const int32_t b = need_b ? bm.batch_of(r) : 0;
+            if (JOIN) {
+                if (a.gate && b != cur_g) {
+#pragma unroll
+                    for (int c = 0; c < NCH; ++c) load_params<E>(a.gate + b * gst + (c * 64 + lane) * E, jg[c]);
+                    cur_g = b;
+                }
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+                    for (int i = 0; i < E; ++i) {
+                        float t = a.bias ? add_rn(hv[k][c][i], jb[c][i]) : hv[k][c][i];
+                        if (a.gate) t = mul_rn(t, jg[c][i]);
+                        v[k][c][i] = round_to<T>(add_rn(v[k][c][i], t));
+                    }
+                    store_elems<T, E, true>(xo + base + (c * 64 + lane) * E, v[k][c]);
+                }
+            }
 
-        const int32_t b = (a.mode == T2H_LN_MODULATE || (JOIN && a.gate)) ? bm.batch_of(r) : 0;
-        if (JOIN) {
-            float hv[NCH][E];
+            float s = 0.0f;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
-            if (a.gate && b != cur_g) {
+            for (int c = 0; c < NCH; ++c)
 #pragma unroll
-                for (int c = 0; c < NCH; ++c) load_params<E>(a.gate + b * gst + (c * 64 + lane) * E, jg[c]);
-                cur_g = b;
+                for (int i = 0; i < E; ++i) s += v[k][c][i];
+            const float mean = wave_sum(s) / (float)C;
+            float q = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+#pragma unroll
+                for (int i = 0; i < E; ++i) {
+                    v[k][c][i] = sub_rn(v[k][c][i], mean);   // keep x - mean for the epilogue
+                    q += v[k][c][i] * v[k][c][i];
+                }
+            const float var = wave_sum(q) / (float)C;
+            const float inv = 1.0f / sqrtf(var + a.eps);
+
+            if (a.mode != T2H_LN_PLAIN) {
+                const int32_t pbx = (a.mode == T2H_LN_MODULATE) ? b : 0;
+                if (pbx != cur_p) {
+#pragma unroll
+                    for (int c = 0; c < NCH; ++c) {
+                        const int col = (c * 64 + lane) * E;
+                        load_params<E>(a.p0 + pbx * pst + col, pa[c]);
+                        load_params<E>(a.p1 + pbx * pst + col, pb[c]);
+                        if (a.mode == T2H_LN_MODULATE) {
+#pragma unroll
+                            for (int i = 0; i < E; ++i) pb[c][i] = add_rn(1.0f, pb[c][i]);   // 1 + scale
+                        }
+                    }
+                    cur_p = pbx;
+                }
             }
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
+                float y[E];
 #pragma unroll
-                for (int i = 0; i < E; ++i) {
-                    float t = a.bias ? add_rn(hv[c][i], jb[c][i]) : hv[c][i];
-                    if (a.gate) t = mul_rn(t, jg[c][i]);
-                    v[c][i] = round_to<T>(add_rn(v[c][i], t));
-                }
-                store_elems<T, E, true>(xo + base + (c * 64 + lane) * E, v[c]);
+                for (int i = 0; i < E; ++i)
+                    y[i] = ln_epilogue(v[k][c][i], inv, a.mode, a.mode != T2H_LN_PLAIN ? pa[c][i] : 0.0f,
+                                       a.mode != T2H_LN_PLAIN ? pb[c][i] : 0.0f);
+                store_elems<T, E, true>(yo + base + (c * 64 + lane) * E, y);
             }
-        }
-
-        float s = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-            for (int i = 0; i < E; ++i) s += v[c][i];
-        const float mean = wave_sum(s) / (float)C;
-        float q = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-            for (int i = 0; i < E; ++i) {
-                const float d = v[c][i] - mean;
-                q += d * d;
-            }
-        const float var = wave_sum(q) / (float)C;
-        const float inv = 1.0f / sqrtf(var + a.eps);
-
-        if (a.mode != T2H_LN_PLAIN) {
-            const int32_t pbx = (a.mode == T2H_LN_MODULATE) ? b : 0;
-            if (pbx != cur_p) {
-#pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    const int col = (c * 64 + lane) * E;
-                    load_params<E>(a.p0 + pbx * pst + col, pa[c]);
-                    load_params<E>(a.p1 + pbx * pst + col, pb[c]);
-                }
-                cur_p = pbx;
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            float y[E];
-#pragma unroll
-            for (int i = 0; i < E; ++i)
-                y[i] = ln_epilogue(v[c][i], mean, inv, a.mode,
-                                   a.mode != T2H_LN_PLAIN ? pa[c][i] : 0.0f,
-                                   a.mode != T2H_LN_PLAIN ? pb[c][i] : 0.0f);
-            store_elems<T, E, true>(yo + base + (c * 64 + lane) * E, y);
         }
     }
 }
@@ -169,7 +190,7 @@ __global__ __launch_bounds__(kBlock) void ln_rows_generic(LnArgs a) {
         const float mean = block_sum(s) / (float)C;
         float q = 0.0f;
         for (int c = tid; c < C; c += kBlock) {
-            const float d = value(c) - mean;
+            const float d = sub_rn(value(c), mean);
             q += d * d;
         }
         const float var = block_sum(q) / (float)C;
@@ -177,8 +198,9 @@ __global__ __launch_bounds__(kBlock) void ln_rows_generic(LnArgs a) {
         const int32_t pbx = (a.mode == T2H_LN_MODULATE) ? b : 0;
         for (int c = tid; c < C; c += kBlock) {
             const float pa = a.mode != T2H_LN_PLAIN ? a.p0[pbx * a.p_stride + c] : 0.0f;
-            const float pb = a.mode != T2H_LN_PLAIN ? a.p1[pbx * a.p_stride + c] : 0.0f;
-            st1(yo + base + c, ln_epilogue(value(c), mean, inv, a.mode, pa, pb));
+            float pb = a.mode != T2H_LN_PLAIN ? a.p1[pbx * a.p_stride + c] : 0.0f;
+            if (a.mode == T2H_LN_MODULATE) pb = add_rn(1.0f, pb);
+            st1(yo + base + c, ln_epilogue(sub_rn(value(c), mean), inv, a.mode, pa, pb));
         }
     }
 }
@@ -192,10 +214,12 @@ int resident_blocks(K kernel) {
 
 template <typename T, int NCH, bool JOIN>
 hipError_t launch_fast(const LnArgs& a, hipStream_t s) {
-    auto k = ln_rows_kernel<T, NCH, JOIN>;
+    // two rows per wave iteration while a row takes <= 3 16-byte loads per lane
+    constexpr int RPW = (NCH * (JOIN ? 2 : 1) <= 3) ? T2H_LN_RPW : 1;
+    auto k = ln_rows_kernel<T, NCH, JOIN, RPW>;
     static const int cap = resident_blocks(k);
-    const int64_t need = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int grid = (int)(need < cap ? need : cap);
+    const int64_t need = (a.rows + kWavesPerBlock * RPW - 1) / (kWavesPerBlock * RPW);
+    const int grid = (int)((T2H_LN_PERSIST && need > cap) ? cap : need);
     hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }

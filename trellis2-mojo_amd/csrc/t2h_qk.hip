@@ -1,15 +1,18 @@
 // Multi-head QK RMSNorm + 3D RoPE (+ qkv bias) on token rows, and the RoPE
 // phase-table builder.
 //
-// Fast path (head_dim 64 or 128, heads <= 16): one wave64 per token row.
+// Fast path (head_dim 64 or 128, heads <= 16): one wave64 per token row and
+// tensor (q or k).
 // Each head is handled by one DPP row of 16 lanes (lane m holds elements
 // [m*E, m*E+E), E = head_dim/16), so a wave instruction covers 4 heads and the
 // per-head sum of squares is a 4-step DPP row sum with no LDS. The interleaved
-// RoPE pairs (2p, 2p+1) are lane-local. Each lane computes cos/sin of its E/2
-// slots once per row from the row's integer voxel coordinates (or the dense
-// grid index, or a precomputed phase table) and reuses them for every head of
-// q and k, so no phase table is read from HBM. Waves are persistent and keep
-// gamma_q/gamma_k in VGPRs across rows.
+// RoPE pairs (2p, 2p+1) are lane-local. q and k of a row go to two waves.
+// Per row and tensor, lane l computes cos/sin of slot l once (64 lanes = the
+// 64 slots of head_dim 128) from the row's integer voxel coordinates (or the
+// dense grid index), and ds_bpermute hands each lane the E/2 slots its pairs
+// need, reused for every head; no phase table is read from HBM. The RMS
+// scale is 1/max(sqrt(ss), 1e-12) from v_rsq_f32. Waves are persistent;
+// gamma * scale for q and k is staged once per block in LDS.
 //
 // Reference: sparse/attention/modules.mojo:37-102 (MultiHeadRMSNorm),
 // modules/rope.mojo:17-88, sparse/attention/rope.mojo:20-134 (RoPE),
@@ -20,6 +23,9 @@
 namespace t2h {
 namespace {
 
+#ifndef T2H_QK_PERSIST
+#define T2H_QK_PERSIST 1
+#endif
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 
@@ -61,113 +67,55 @@ __device__ __forceinline__ void slot_phase(const float* pos, int ax, float freq,
     }
 }
 
+__device__ __forceinline__ float lane_bcast(float v, int src_lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
+}
+
+// One work unit = one tensor (q, k, or the packed qkv's v) of one token row;
+// units of a row are adjacent, so the waves that share a row's coords run
+// together. A lane's data is E elements of each of NG head groups (24 VGPRs
+// for 12 x 128), which keeps occupancy high enough to overlap one wave's
+// math with other waves' loads.
 template <typename T, int D, int NG>
 __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab) {
-    constexpr int E = D / 16;   // elements per lane per head
-    constexpr int P = E / 2;    // rotary slots per lane
+    constexpr int E = D / 16;      // elements per lane per head
+    constexpr int P = E / 2;       // rotary slots per lane
+    constexpr int HALF = D / 2;    // slots per row (<= 64: one per lane)
+    // gamma * scale for q then k, staged once per block
+    __shared__ __attribute__((aligned(16))) float gs[2 * NG * 4 * D];
     const int lane = lane_id();
     const int g = lane >> 4;
     const int m = lane & 15;
     const int H = a.heads;
     const int64_t HD = (int64_t)H * D;
-    const T* __restrict__ qi = static_cast<const T*>(a.q_in);
-    const T* __restrict__ ki = static_cast<const T*>(a.k_in);
-    T* __restrict__ qo = static_cast<T*>(a.q_out);
-    T* __restrict__ ko = static_cast<T*>(a.k_out);
     const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
-    const bool rms = a.gamma_q != nullptr || a.gamma_k != nullptr;
     const float sc = a.rms_scale;
 
-    // lane-constant slot table and gammas
-    float sf[P];
-    int sa[P];
-#pragma unroll
-    for (int t = 0; t < P; ++t) {
-        sf[t] = tab.freq[m * P + t];
-        sa[t] = tab.axis[m * P + t];
+    for (int i = threadIdx.x; i < 2 * NG * 4 * D; i += kBlock) {
+        const int which = i / (NG * 4 * D), e = i % (NG * 4 * D);
+        const float* gm = which == 0 ? a.gamma_q : a.gamma_k;
+        gs[i] = (gm != nullptr && e < HD) ? gm[e] * sc : sc;
     }
-    float gq[NG][E], gk[NG][E];
-#pragma unroll
-    for (int it = 0; it < NG; ++it) {
-        const int hh = 4 * it + g;
-        const int64_t off = (int64_t)hh * D + m * E;
-#pragma unroll
-        for (int i = 0; i < E; ++i) { gq[it][i] = 1.0f; gk[it][i] = 1.0f; }
-        if (hh < H) {
-            if (a.gamma_q) load_params<E>(a.gamma_q + off, gq[it]);
-            if (a.gamma_k) load_params<E>(a.gamma_k + off, gk[it]);
-        }
-    }
+    __syncthreads();
 
+    // this lane computes the phase of slot `lane` (lanes >= HALF mirror lane - HALF)
+    const int my_slot = lane % HALF;
+    const float my_freq = tab.freq[my_slot];
+    const int my_axis = tab.axis[my_slot];
+
+    // units per row: q, k (each optional) and the packed v (bias only)
+    const int has_q = a.q_in != nullptr, has_k = a.k_in != nullptr;
+    const int has_v = a.v != nullptr && a.bias_v != nullptr;
+    const int upr = has_q + has_k + has_v;
+    const int64_t units = a.rows * upr;
     const int64_t nwaves = (int64_t)gridDim.x * kWaves;
-    for (int64_t r = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); r < a.rows; r += nwaves) {
-        float qv[NG][E], kv[NG][E];
-#pragma unroll
-        for (int it = 0; it < NG; ++it) {
-            const int hh = 4 * it + g;
-            const int64_t off = r * a.in_stride + (int64_t)hh * D + m * E;
-#pragma unroll
-            for (int i = 0; i < E; ++i) { qv[it][i] = 0.0f; kv[it][i] = 0.0f; }
-            if (hh < H) {
-                if (qi) load_elems<T, E, true>(qi + off, qv[it]);
-                if (ki) load_elems<T, E, true>(ki + off, kv[it]);
-            }
-        }
+    for (int64_t u = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); u < units; u += nwaves) {
+        const int64_t r = u / upr;
+        int which = (int)(u - r * upr);
+        if (!has_q) ++which;            // 0 = q, 1 = k, 2 = v
+        if (which == 1 && !has_k) ++which;
 
-        float pc[P], ps[P];
-        if (a.use_rope) {
-            if (a.phases != nullptr) {
-                const int64_t l = r % a.phase_rows;
-                float tmp[2 * P];  // P interleaved (cos, sin) pairs
-                load_params<2 * P>(a.phases + (l * (D / 2) + m * P) * 2, tmp);
-#pragma unroll
-                for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
-            } else {
-                float pos[T2H_MAX_POS_DIM];
-                src.get(r, pos);
-#pragma unroll
-                for (int t = 0; t < P; ++t) slot_phase(pos, sa[t], sf[t], pc[t], ps[t]);
-            }
-        }
-
-        auto process = [&](float (&v)[NG][E], const float (&gm)[NG][E], const float* bias,
-                           bool has_gamma, T* __restrict__ out) {
-#pragma unroll
-            for (int it = 0; it < NG; ++it) {
-                const int hh = 4 * it + g;
-                const bool valid = hh < H;
-                if (bias != nullptr && valid) {
-                    float bv[E];
-                    load_params<E>(bias + (int64_t)hh * D + m * E, bv);
-#pragma unroll
-                    for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
-                }
-                if (has_gamma) {
-                    float ss = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < E; ++i) ss += v[it][i] * v[it][i];
-                    ss = row16_sum(ss);
-                    float nrm = sqrtf(ss);
-                    if (nrm < 1e-12f) nrm = 1e-12f;
-                    const float rn = 1.0f / nrm;
-#pragma unroll
-                    for (int i = 0; i < E; ++i) v[it][i] = v[it][i] * rn * gm[it][i] * sc;
-                }
-                if (a.use_rope) {
-#pragma unroll
-                    for (int t = 0; t < P; ++t) {
-                        const float re = v[it][2 * t], im = v[it][2 * t + 1];
-                        v[it][2 * t] = re * pc[t] - im * ps[t];
-                        v[it][2 * t + 1] = re * ps[t] + im * pc[t];
-                    }
-                }
-                if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
-            }
-        };
-        if (qi) process(qv, gq, a.bias_q, rms && a.gamma_q != nullptr, qo);
-        if (ki) process(kv, gk, a.bias_k, rms && a.gamma_k != nullptr, ko);
-
-        if (a.v != nullptr && a.bias_v != nullptr) {  // packed qkv: v += bias_v
+        if (which == 2) {               // packed qkv: v += bias_v
             T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
             for (int64_t e0 = (int64_t)lane * E; e0 < HD; e0 += 64 * E) {
                 float vv[E], bv[E];
@@ -177,6 +125,79 @@ __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab
                 for (int i = 0; i < E; ++i) vv[i] = add_rn(vv[i], bv[i]);
                 store_elems<T, E>(vr + e0, vv);
             }
+            continue;
+        }
+        const T* __restrict__ in = static_cast<const T*>(which == 0 ? a.q_in : a.k_in);
+        T* __restrict__ out = static_cast<T*>(which == 0 ? a.q_out : a.k_out);
+        const float* bias = which == 0 ? a.bias_q : a.bias_k;
+        const bool has_gamma = (which == 0 ? a.gamma_q : a.gamma_k) != nullptr;
+
+        float v[NG][E];
+#pragma unroll
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+#pragma unroll
+            for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
+            if (hh < H) load_elems<T, E, true>(in + r * a.in_stride + (int64_t)hh * D + m * E, v[it]);
+        }
+
+        float pc[P], ps[P];
+        if (a.use_rope) {
+            if (a.phases != nullptr) {
+                const int64_t l = r % a.phase_rows;
+                float tmp[2 * P];  // P interleaved (cos, sin) pairs
+                load_params<2 * P>(a.phases + (l * HALF + m * P) * 2, tmp);
+#pragma unroll
+                for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
+            } else {
+                float pos[T2H_MAX_POS_DIM];
+                src.get(r, pos);
+                float c, s;
+                slot_phase(pos, my_axis, my_freq, c, s);
+#pragma unroll
+                for (int t = 0; t < P; ++t) {   // slot m*P + t lives in lane m*P + t
+                    pc[t] = lane_bcast(c, m * P + t);
+                    ps[t] = lane_bcast(s, m * P + t);
+                }
+            }
+        }
+
+#pragma unroll
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+            const bool valid = hh < H;
+            if (bias != nullptr && valid) {
+                float bv[E];
+                load_params<E>(bias + (int64_t)hh * D + m * E, bv);
+#pragma unroll
+                for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
+            }
+            if (has_gamma) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < E; ++i) ss += v[it][i] * v[it][i];
+                ss = row16_sum(ss);
+                // 1 / max(sqrt(ss), 1e-12): sqrt(ss) < 1e-12 <=> ss < 1e-24
+                const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+                float gv[E];
+                const float4* gp = reinterpret_cast<const float4*>(&gs[(which * NG * 4 + hh) * D + m * E]);
+#pragma unroll
+                for (int c4 = 0; c4 < E / 4; ++c4) {
+                    const float4 w = gp[c4];
+                    gv[4 * c4] = w.x; gv[4 * c4 + 1] = w.y; gv[4 * c4 + 2] = w.z; gv[4 * c4 + 3] = w.w;
+                }
+#pragma unroll
+                for (int i = 0; i < E; ++i) v[it][i] = (v[it][i] * rn) * gv[i];
+            }
+            if (a.use_rope) {
+#pragma unroll
+                for (int t = 0; t < P; ++t) {
+                    const float re = v[it][2 * t], im = v[it][2 * t + 1];
+                    v[it][2 * t] = re * pc[t] - im * ps[t];
+                    v[it][2 * t + 1] = re * ps[t] + im * pc[t];
+                }
+            }
+            if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
         }
     }
 }
@@ -285,8 +306,9 @@ template <typename T, int D, int NG>
 hipError_t launch_fast(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
     auto k = qk_rows_kernel<T, D, NG>;
     static const int cap = resident_blocks(k);
-    const int64_t need = (a.rows + kWaves - 1) / kWaves;
-    const int grid = (int)(need < cap ? need : cap);
+    const int upr = (a.q_in != nullptr) + (a.k_in != nullptr) + (a.v != nullptr && a.bias_v != nullptr);
+    const int64_t need = (a.rows * upr + kWaves - 1) / kWaves;
+    const int grid = (int)((T2H_QK_PERSIST && need > cap) ? cap : need);
     hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a, tab);
     return hipGetLastError();
 }
