@@ -112,8 +112,8 @@ class Chain:
             return lambda: o.activation(self.u, o.ACT_GELU_TANH, bias=self.bias, out=self.gout)
         if name == "gate_residual":
             return lambda: o.gate_residual(self.x, self.y, gate=self.gate, offsets=self.offsets, out=self.res)
-        if name == "copy":  # calibration: a plain device copy of the GELU tensor (torch's copy kernel)
-            return lambda: self.gout.copy_(self.u)
+        if name == "copy":  # calibration: torch's vectorized elementwise kernel copying the GELU tensor (y = x * 1)
+            return lambda: self.torch.mul(self.u, 1.0, out=self.gout)
         if name == "chain":
             return self.step
         raise KeyError(name)

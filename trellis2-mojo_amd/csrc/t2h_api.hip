@@ -308,6 +308,7 @@ static int32_t qk_common(const void* q_in, const void* k_in, void* q_out, void* 
     a.rms_scale = (float)std::pow((double)head_dim, 0.5);  // Float32(Float64(dim) ** 0.5)
     a.use_rope = use_rope ? 1 : 0;
     a.pos_dim = pos_dim;
+    a.freq_dim = use_rope ? freq_dim : 0;
     a.phases = use_rope ? phases : nullptr;
     a.phase_rows = phase_rows;
     a.coords = (use_rope && phases == nullptr) ? coords : nullptr;

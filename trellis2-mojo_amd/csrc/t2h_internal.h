@@ -62,6 +62,7 @@ struct QkArgs {
     float rms_scale;         // f32(sqrt(f64(head_dim)))
     int32_t use_rope;
     int32_t pos_dim;
+    int32_t freq_dim;        // distinct rotary frequencies (slot p uses freq p % freq_dim)
     const float* phases;     // position source 1
     int64_t phase_rows;
     const int32_t* coords;   // position source 2

@@ -103,19 +103,22 @@ __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab
     const float my_freq = tab.freq[my_slot];
     const int my_axis = tab.axis[my_slot];
 
-    // units per row: q, k (each optional) and the packed v (bias only)
+    // units per row: q, k (each optional) and the packed v (bias only). Each
+    // wave owns one of them for its whole life (which = wave % upr) and walks
+    // rows with a constant stride (the grid's wave count is a multiple of upr).
     const int has_q = a.q_in != nullptr, has_k = a.k_in != nullptr;
     const int has_v = a.v != nullptr && a.bias_v != nullptr;
     const int upr = has_q + has_k + has_v;
-    const int64_t units = a.rows * upr;
+    const int64_t wave = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t nwaves = (int64_t)gridDim.x * kWaves;
-    for (int64_t u = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); u < units; u += nwaves) {
-        const int64_t r = u / upr;
-        int which = (int)(u - r * upr);
-        if (!has_q) ++which;            // 0 = q, 1 = k, 2 = v
-        if (which == 1 && !has_k) ++which;
+    int which = (int)(wave % upr);
+    if (!has_q) ++which;            // 0 = q, 1 = k, 2 = v
+    if (which == 1 && !has_k) ++which;
+    const int64_t row_step = nwaves / upr;
+    const int64_t row0 = wave / upr;
 
-        if (which == 2) {               // packed qkv: v += bias_v
+    if (which == 2) {               // packed qkv: v += bias_v
+        for (int64_t r = row0; r < a.rows; r += row_step) {
             T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
             for (int64_t e0 = (int64_t)lane * E; e0 < HD; e0 += 64 * E) {
                 float vv[E], bv[E];
@@ -125,13 +128,25 @@ __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab
                 for (int i = 0; i < E; ++i) vv[i] = add_rn(vv[i], bv[i]);
                 store_elems<T, E>(vr + e0, vv);
             }
-            continue;
         }
-        const T* __restrict__ in = static_cast<const T*>(which == 0 ? a.q_in : a.k_in);
-        T* __restrict__ out = static_cast<T*>(which == 0 ? a.q_out : a.k_out);
-        const float* bias = which == 0 ? a.bias_q : a.bias_k;
-        const bool has_gamma = (which == 0 ? a.gamma_q : a.gamma_k) != nullptr;
+        return;
+    }
+    const T* __restrict__ in = static_cast<const T*>(which == 0 ? a.q_in : a.k_in);
+    T* __restrict__ out = static_cast<T*>(which == 0 ? a.q_out : a.k_out);
+    const float* __restrict__ bias = which == 0 ? a.bias_q : a.bias_k;
+    const bool has_gamma = (which == 0 ? a.gamma_q : a.gamma_k) != nullptr;
+    const float* __restrict__ gsw = gs + which * NG * 4 * D;
 
+    const bool coord_pos = a.use_rope && a.phases == nullptr && a.coords != nullptr;
+    // The coordinate this lane's slot rotates by (pad slots: none) for row r,
+    // loaded one row ahead, so the phase math never waits on a load.
+    auto slot_coord = [&](int64_t r) -> float {
+        if (!coord_pos || r >= a.rows || my_axis < 0) return 0.0f;
+        return (float)a.coords[r * a.coord_cols + 1 + my_axis];
+    };
+    float cpos = slot_coord(row0);
+    for (int64_t r = row0; r < a.rows; r += row_step) {
+        const float npos = slot_coord(r + row_step);
         float v[NG][E];
 #pragma unroll
         for (int it = 0; it < NG; ++it) {
@@ -150,8 +165,8 @@ __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab
 #pragma unroll
                 for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
             } else {
-                float pos[T2H_MAX_POS_DIM];
-                src.get(r, pos);
+                float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};   // this lane's slot axis only
+                if (!coord_pos) src.get(r, pos);
                 float c, s;
                 slot_phase(pos, my_axis, my_freq, c, s);
 #pragma unroll
@@ -180,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab
                 // 1 / max(sqrt(ss), 1e-12): sqrt(ss) < 1e-12 <=> ss < 1e-24
                 const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
                 float gv[E];
-                const float4* gp = reinterpret_cast<const float4*>(&gs[(which * NG * 4 + hh) * D + m * E]);
+                const float4* gp = reinterpret_cast<const float4*>(&gsw[hh * D + m * E]);
 #pragma unroll
                 for (int c4 = 0; c4 < E / 4; ++c4) {
                     const float4 w = gp[c4];
@@ -199,6 +214,7 @@ __global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab
             }
             if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
         }
+        cpos = npos;
     }
 }
 
@@ -308,7 +324,9 @@ hipError_t launch_fast(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
     static const int cap = resident_blocks(k);
     const int upr = (a.q_in != nullptr) + (a.k_in != nullptr) + (a.v != nullptr && a.bias_v != nullptr);
     const int64_t need = (a.rows * upr + kWaves - 1) / kWaves;
-    const int grid = (int)((T2H_QK_PERSIST && need > cap) ? cap : need);
+    int grid = (int)((T2H_QK_PERSIST && need > cap) ? cap : need);
+    // the kernel gives each wave one tensor: the wave count must be a multiple of upr
+    while ((grid * (int64_t)kWaves) % upr != 0) ++grid;
     hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a, tab);
     return hipGetLastError();
 }
