@@ -169,6 +169,15 @@ int32_t t2h_qkv_bias_rmsnorm_rope(void* qkv, int64_t rows, int32_t heads,
                                   int32_t coord_cols, int32_t grid_res,
                                   void* stream);
 
+/* Host function (no device work): the embedders' frequency table
+ * freqs[j] = f32(freq_lo) / f32(freq_hi) ** (f32(j) / f32(freq_dim)),
+ * freq_dim = head_dim / 2 / dim, in f32 with libm powf — the constructor of
+ * RotaryPositionEmbedder / SparseRotaryPositionEmbedder (modules/rope.mojo:
+ * 24-37, sparse/attention/rope.mojo:26-39). Writes min(freq_dim, capacity)
+ * entries and returns freq_dim, or a negative status (odd head_dim). */
+int32_t t2h_rope_freqs(int32_t head_dim, int32_t dim, double freq_lo,
+                       double freq_hi, float* freqs_host, int32_t capacity);
+
 /* Phase table [rows, head_dim/2, 2] f32 (cos, sin): replaces
  * RotaryPositionEmbedder.forward (modules/rope.mojo:39-61; positions f32
  * [rows, pos_dim]) and SparseRotaryPositionEmbedder._compute_phases

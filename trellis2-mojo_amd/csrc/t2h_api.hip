@@ -346,6 +346,20 @@ int32_t t2h_qkv_bias_rmsnorm_rope(void* qkv, int64_t rows, int32_t heads, int32_
                      freqs_host, freq_dim, pos_dim, phases, phase_rows, coords, coord_cols, grid_res, stream, fn);
 }
 
+int32_t t2h_rope_freqs(int32_t head_dim, int32_t dim, double freq_lo, double freq_hi, float* freqs_host,
+                       int32_t capacity) {
+    if (head_dim <= 0 || head_dim % 2 != 0)
+        return fail(T2H_EINVAL, "RotaryPositionEmbedder: head_dim must be even");
+    if (dim <= 0) return fail(T2H_EINVAL, "t2h_rope_freqs: dim must be > 0");
+    const int32_t fd = head_dim / 2 / dim;
+    for (int32_t j = 0; j < fd && j < capacity; ++j) {
+        const float e = (float)j / (float)fd;
+        freqs_host[j] = (float)freq_lo / std::pow((float)freq_hi, e);   // powf, as the constructor's f32 **
+    }
+    ok();
+    return fd;
+}
+
 int32_t t2h_rope_phases(float* phases_out, int64_t rows, int32_t head_dim, const float* freqs_host, int32_t freq_dim,
                         int32_t pos_dim, const float* positions, const int32_t* coords, int32_t coord_cols,
                         int32_t grid_res, void* stream) {

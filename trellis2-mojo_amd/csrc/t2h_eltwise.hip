@@ -79,6 +79,10 @@ struct Tile {
     int64_t col0;
     int64_t r0;
     int nrows;
+    // Row k of the tile for loads, clamped to the tile's last row: every load
+    // is unconditional (so all kRpt loads are in flight together) and only the
+    // stores check k < nrows.
+    __device__ __forceinline__ int64_t row(int k) const { return r0 + (k < nrows ? k : nrows - 1); }
 };
 
 // Tile of this block, 1-D grid. When a row is a whole number of waves of
@@ -112,6 +116,9 @@ __global__ __launch_bounds__(1024) void act_kernel(EltArgs a) {
     T* __restrict__ o = static_cast<T*>(a.out);
     float bias[V];
     if (BIAS) ldp<V>(a.bias + t.col0, bias);
+    // Row loads stay conditional here: one load in flight per thread and row,
+    // overlapped with the previous row's math, streams faster for this kernel
+    // than issuing all kRpt loads up front (measured on MI355X).
     float v[kRpt][V];
 #pragma unroll
     for (int k = 0; k < kRpt; ++k)
@@ -137,14 +144,13 @@ __global__ __launch_bounds__(1024) void gate_res_kernel(EltArgs a) {
     float bias[V], g[V];
     if (a.bias) ldp<V>(a.bias + t.col0, bias);
     int32_t cur = -1;
+    const T* __restrict__ xs = x != nullptr ? x : h;   // without x: a second (ignored) read of h
     float hv[kRpt][V], xv[kRpt][V];
 #pragma unroll
     for (int k = 0; k < kRpt; ++k) {
-        if (k < t.nrows) {
-            const int64_t off = (t.r0 + k) * a.cols + t.col0;
-            ld<T, V>(h + off, hv[k]);
-            if (x) ld<T, V>(x + off, xv[k]);
-        }
+        const int64_t off = t.row(k) * a.cols + t.col0;
+        ld<T, V>(h + off, hv[k]);
+        ld<T, V>(xs + off, xv[k]);
     }
 #pragma unroll
     for (int k = 0; k < kRpt; ++k) {
@@ -176,8 +182,7 @@ __global__ __launch_bounds__(1024) void modulate_kernel(EltArgs a) {
     int32_t cur = -1;
     float v[kRpt][V];
 #pragma unroll
-    for (int k = 0; k < kRpt; ++k)
-        if (k < t.nrows) ld<T, V>(x + (t.r0 + k) * a.cols + t.col0, v[k]);
+    for (int k = 0; k < kRpt; ++k) ld<T, V>(x + t.row(k) * a.cols + t.col0, v[k]);
 #pragma unroll
     for (int k = 0; k < kRpt; ++k) {
         if (k >= t.nrows) break;
@@ -219,8 +224,7 @@ __global__ __launch_bounds__(1024) void binop_kernel(EltArgs a) {
     int32_t cur = -1;
     float v[kRpt][V];
 #pragma unroll
-    for (int k = 0; k < kRpt; ++k)
-        if (k < t.nrows) ld<T, V>(x + (t.r0 + k) * a.cols + t.col0, v[k]);
+    for (int k = 0; k < kRpt; ++k) ld<T, V>(x + t.row(k) * a.cols + t.col0, v[k]);
 #pragma unroll
     for (int k = 0; k < kRpt; ++k) {
         if (k >= t.nrows) break;

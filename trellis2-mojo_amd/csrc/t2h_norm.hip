@@ -3,11 +3,12 @@
 //
 // Fast path: one wave64 per row, the row held in VGPRs (C = 64 * NCH * E with
 // E = 16 B of storage per lane, e.g. C = 1536: f32 NCH 6, f16/bf16 NCH 3), so
-// the two-pass mean/variance never re-reads HBM. Waves are persistent and
-// stride over rows; the per-batch parameter rows (shift/scale, gate) stay in
-// VGPRs until the row's batch changes. Reductions are DPP row sums plus four
-// readlanes. Every output element follows the reference's f32 rounding
-// sequence; only the order of the two row sums differs from the reference.
+// the two-pass mean/variance never re-reads HBM. The grid has one wave per row
+// (not persistent: many short waves stream HBM better on MI355X), and the
+// per-batch parameter rows are read through L1 at use. Reductions are DPP row
+// sums plus four readlanes. Every output element follows the reference's f32
+// rounding sequence; only the order of the two row sums differs from the
+// reference.
 //
 // Reference: modules/nn.mojo:314-369 (LayerNorm32), 660-689 (modulate),
 // sparse/transformer/modulated.mojo:60-65 (gathered modulate),
@@ -18,12 +19,6 @@
 namespace t2h {
 namespace {
 
-#ifndef T2H_LN_RPW
-#define T2H_LN_RPW 2
-#endif
-#ifndef T2H_LN_PERSIST
-#define T2H_LN_PERSIST 1
-#endif
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = 64 * kWavesPerBlock;
 
@@ -37,113 +32,84 @@ __device__ __forceinline__ float ln_epilogue(float d, float inv, int mode, float
     return n;
 }
 
-template <typename T, int NCH, bool JOIN, int RPW>
+template <typename T, int NCH, bool JOIN>
 __global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
     constexpr int E = kPack<T>;
     constexpr int C = 64 * NCH * E;
     const int lane = lane_id();
-    const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    const int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (r >= a.rows) return;
     const T* __restrict__ x = static_cast<const T*>(a.x);
     const T* __restrict__ h = static_cast<const T*>(a.h);
     T* __restrict__ xo = static_cast<T*>(a.x_out);
     T* __restrict__ yo = static_cast<T*>(a.y_out);
-    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
-    const int64_t pst = a.p_stride;
-    const int64_t gst = a.gate_stride;
+    const int64_t base = r * (int64_t)C;
     const bool need_b = a.mode == T2H_LN_MODULATE || (JOIN && a.gate);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
 
-    float pa[NCH][E], pb[NCH][E];   // epilogue params of batch cur_p
-    float jb[NCH][E], jg[NCH][E];   // join bias (fixed) and gate of batch cur_g
-    int32_t cur_p = -1, cur_g = -1;
-    if (JOIN && a.bias) {
+    float v[NCH][E];
+    float hv[NCH][E];
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) load_params<E>(a.bias + (c * 64 + lane) * E, jb[c]);
+    for (int c = 0; c < NCH; ++c) {
+        load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
+        if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
+    }
+    const int32_t b = need_b ? bm.batch_of(r) : 0;
+
+    if (JOIN) {   // x_out = x + fl(fl(h + bias) * gate[b]), as stored in T
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int col = (c * 64 + lane) * E;
+            float jb[E], jg[E];
+            if (a.bias) load_params<E>(a.bias + col, jb);
+            if (a.gate) load_params<E>(a.gate + b * a.gate_stride + col, jg);
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                float t = a.bias ? add_rn(hv[c][i], jb[i]) : hv[c][i];
+                if (a.gate) t = mul_rn(t, jg[i]);
+                v[c][i] = round_to<T>(add_rn(v[c][i], t));
+            }
+            store_elems<T, E, true>(xo + base + col, v[c]);
+        }
     }
 
-    // RPW consecutive rows per wave per iteration: all their loads are issued
-    // before any reduction, so each wave keeps RPW rows in flight.
-    const int64_t wave = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-    for (int64_t r0 = wave * RPW; r0 < a.rows; r0 += nwaves * RPW) {
-        float v[RPW][NCH][E];
-        float hv[RPW][NCH][E];
+    float s = 0.0f;
 #pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            if (r0 + k < a.rows) {
-                const int64_t base = (r0 + k) * (int64_t)C;
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[k][c]);
-                    if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[k][c]);
-                }
-            }
+        for (int i = 0; i < E; ++i) s += v[c][i];
+    const float mean = wave_sum(s) / (float)C;
+    float q = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            v[c][i] = sub_rn(v[c][i], mean);   // keep x - mean for the epilogue
+            q += v[c][i] * v[c][i];
         }
-#pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            const int64_t r = r0 + k;
-            if (r >= a.rows) break;
-            const int64_t base = r * (int64_t)C;
-            const int32_t b = need_b ? bm.batch_of(r) : 0;
-            if (JOIN) {
-                if (a.gate && b != cur_g) {
-#pragma unroll
-                    for (int c = 0; c < NCH; ++c) load_params<E>(a.gate + b * gst + (c * 64 + lane) * E, jg[c]);
-                    cur_g = b;
-                }
-#pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-#pragma unroll
-                    for (int i = 0; i < E; ++i) {
-                        float t = a.bias ? add_rn(hv[k][c][i], jb[c][i]) : hv[k][c][i];
-                        if (a.gate) t = mul_rn(t, jg[c][i]);
-                        v[k][c][i] = round_to<T>(add_rn(v[k][c][i], t));
-                    }
-                    store_elems<T, E, true>(xo + base + (c * 64 + lane) * E, v[k][c]);
-                }
-            }
+    const float var = wave_sum(q) / (float)C;
+    const float inv = 1.0f / sqrtf(var + a.eps);
 
-            float s = 0.0f;
+    const int32_t pb_row = (a.mode == T2H_LN_MODULATE) ? b : 0;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c)
+    for (int c = 0; c < NCH; ++c) {
+        const int col = (c * 64 + lane) * E;
+        float pa[E], pb[E];
+        if (a.mode != T2H_LN_PLAIN) {   // per-chunk parameter rows, read through L1 at use
+            load_params<E>(a.p0 + pb_row * a.p_stride + col, pa);
+            load_params<E>(a.p1 + pb_row * a.p_stride + col, pb);
+            if (a.mode == T2H_LN_MODULATE) {
 #pragma unroll
-                for (int i = 0; i < E; ++i) s += v[k][c][i];
-            const float mean = wave_sum(s) / (float)C;
-            float q = 0.0f;
-#pragma unroll
-            for (int c = 0; c < NCH; ++c)
-#pragma unroll
-                for (int i = 0; i < E; ++i) {
-                    v[k][c][i] = sub_rn(v[k][c][i], mean);   // keep x - mean for the epilogue
-                    q += v[k][c][i] * v[k][c][i];
-                }
-            const float var = wave_sum(q) / (float)C;
-            const float inv = 1.0f / sqrtf(var + a.eps);
-
-            if (a.mode != T2H_LN_PLAIN) {
-                const int32_t pbx = (a.mode == T2H_LN_MODULATE) ? b : 0;
-                if (pbx != cur_p) {
-#pragma unroll
-                    for (int c = 0; c < NCH; ++c) {
-                        const int col = (c * 64 + lane) * E;
-                        load_params<E>(a.p0 + pbx * pst + col, pa[c]);
-                        load_params<E>(a.p1 + pbx * pst + col, pb[c]);
-                        if (a.mode == T2H_LN_MODULATE) {
-#pragma unroll
-                            for (int i = 0; i < E; ++i) pb[c][i] = add_rn(1.0f, pb[c][i]);   // 1 + scale
-                        }
-                    }
-                    cur_p = pbx;
-                }
+                for (int i = 0; i < E; ++i) pb[i] = add_rn(1.0f, pb[i]);   // 1 + scale
             }
+        } else {
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                float y[E];
-#pragma unroll
-                for (int i = 0; i < E; ++i)
-                    y[i] = ln_epilogue(v[k][c][i], inv, a.mode, a.mode != T2H_LN_PLAIN ? pa[c][i] : 0.0f,
-                                       a.mode != T2H_LN_PLAIN ? pb[c][i] : 0.0f);
-                store_elems<T, E, true>(yo + base + (c * 64 + lane) * E, y);
-            }
+            for (int i = 0; i < E; ++i) { pa[i] = 0.0f; pb[i] = 0.0f; }
         }
+        float y[E];
+#pragma unroll
+        for (int i = 0; i < E; ++i) y[i] = ln_epilogue(v[c][i], inv, a.mode, pa[i], pb[i]);
+        store_elems<T, E, true>(yo + base + col, y);
     }
 }
 
@@ -214,13 +180,8 @@ int resident_blocks(K kernel) {
 
 template <typename T, int NCH, bool JOIN>
 hipError_t launch_fast(const LnArgs& a, hipStream_t s) {
-    // two rows per wave iteration while a row takes <= 3 16-byte loads per lane
-    constexpr int RPW = (NCH * (JOIN ? 2 : 1) <= 3) ? T2H_LN_RPW : 1;
-    auto k = ln_rows_kernel<T, NCH, JOIN, RPW>;
-    static const int cap = resident_blocks(k);
-    const int64_t need = (a.rows + kWavesPerBlock * RPW - 1) / (kWavesPerBlock * RPW);
-    const int grid = (int)((T2H_LN_PERSIST && need > cap) ? cap : need);
-    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a);
+    const int64_t grid = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
+    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), dim3((unsigned)grid), dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }
 

@@ -1,18 +1,24 @@
 // Multi-head QK RMSNorm + 3D RoPE (+ qkv bias) on token rows, and the RoPE
 // phase-table builder.
 //
-// Fast path (head_dim 64 or 128, heads <= 16): one wave64 per token row and
-// tensor (q or k).
-// Each head is handled by one DPP row of 16 lanes (lane m holds elements
-// [m*E, m*E+E), E = head_dim/16), so a wave instruction covers 4 heads and the
-// per-head sum of squares is a 4-step DPP row sum with no LDS. The interleaved
-// RoPE pairs (2p, 2p+1) are lane-local. q and k of a row go to two waves.
-// Per row and tensor, lane l computes cos/sin of slot l once (64 lanes = the
-// 64 slots of head_dim 128) from the row's integer voxel coordinates (or the
-// dense grid index), and ds_bpermute hands each lane the E/2 slots its pairs
-// need, reused for every head; no phase table is read from HBM. The RMS
-// scale is 1/max(sqrt(ss), 1e-12) from v_rsq_f32. Waves are persistent;
-// gamma * scale for q and k is staged once per block in LDS.
+// Fast path (head_dim 64 or 128, heads <= 16): a block of kTileWaves waves
+// handles kTileWaves consecutive token rows of one tensor (q, k, or the packed
+// qkv's v); blocks for the tensors of a row tile are adjacent, so they share
+// the tile's coords in cache. Each head is one DPP row of 16 lanes (lane m
+// holds elements [m*E, m*E+E), E = head_dim/16), so a wave instruction
+// covers 4 heads and the per-head sum of squares is a 4-step DPP row sum.
+// The interleaved RoPE pairs (2p, 2p+1) are lane-local: lane l computes
+// cos/sin of slot l once per row (64 lanes = the 64 slots of head_dim 128)
+// from the row's integer voxel coordinate (or the dense grid index), and
+// ds_bpermute hands each lane the E/2 slots its pairs need; no phase table is
+// read from HBM. The RMS scale is 1/max(sqrt(ss), 1e-12) from v_rsq_f32.
+//
+// Order inside a wave: slot-coordinate load, then the row loads (all
+// unconditional, so they are in flight together), then the block stages the
+// tensor's gamma * scale into LDS and meets at an LDS-only barrier
+// (lgkmcnt(0) + s_barrier, no vmcnt wait: the row loads stay in flight across
+// it). The grid is not persistent: many short blocks stream HBM better on
+// MI355X than waves that loop over rows.
 //
 // Reference: sparse/attention/modules.mojo:37-102 (MultiHeadRMSNorm),
 // modules/rope.mojo:17-88, sparse/attention/rope.mojo:20-134 (RoPE),
@@ -23,9 +29,6 @@
 namespace t2h {
 namespace {
 
-#ifndef T2H_QK_PERSIST
-#define T2H_QK_PERSIST 1
-#endif
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 
@@ -71,150 +74,132 @@ __device__ __forceinline__ float lane_bcast(float v, int src_lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
 }
 
-// One work unit = one tensor (q, k, or the packed qkv's v) of one token row;
-// units of a row are adjacent, so the waves that share a row's coords run
-// together. A lane's data is E elements of each of NG head groups (24 VGPRs
-// for 12 x 128), which keeps occupancy high enough to overlap one wave's
-// math with other waves' loads.
+constexpr int kTileWaves = 8;
+constexpr int kTileBlock = kTileWaves * 64;
+
 template <typename T, int D, int NG>
-__global__ __launch_bounds__(kBlock) void qk_rows_kernel(QkArgs a, RopeSlots tab) {
-    constexpr int E = D / 16;      // elements per lane per head
-    constexpr int P = E / 2;       // rotary slots per lane
-    constexpr int HALF = D / 2;    // slots per row (<= 64: one per lane)
-    // gamma * scale for q then k, staged once per block
-    __shared__ __attribute__((aligned(16))) float gs[2 * NG * 4 * D];
+__global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots tab) {
+    constexpr int E = D / 16;
+    constexpr int P = E / 2;
+    constexpr int HALF = D / 2;
+    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];
     const int lane = lane_id();
     const int g = lane >> 4;
     const int m = lane & 15;
     const int H = a.heads;
-    const int64_t HD = (int64_t)H * D;
-    const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
-    const float sc = a.rms_scale;
-
-    for (int i = threadIdx.x; i < 2 * NG * 4 * D; i += kBlock) {
-        const int which = i / (NG * 4 * D), e = i % (NG * 4 * D);
-        const float* gm = which == 0 ? a.gamma_q : a.gamma_k;
-        gs[i] = (gm != nullptr && e < HD) ? gm[e] * sc : sc;
-    }
-    __syncthreads();
-
-    // this lane computes the phase of slot `lane` (lanes >= HALF mirror lane - HALF)
-    const int my_slot = lane % HALF;
-    const float my_freq = tab.freq[my_slot];
-    const int my_axis = tab.axis[my_slot];
-
-    // units per row: q, k (each optional) and the packed v (bias only). Each
-    // wave owns one of them for its whole life (which = wave % upr) and walks
-    // rows with a constant stride (the grid's wave count is a multiple of upr).
+    const int HD = H * D;
     const int has_q = a.q_in != nullptr, has_k = a.k_in != nullptr;
     const int has_v = a.v != nullptr && a.bias_v != nullptr;
     const int upr = has_q + has_k + has_v;
-    const int64_t wave = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t nwaves = (int64_t)gridDim.x * kWaves;
-    int which = (int)(wave % upr);
-    if (!has_q) ++which;            // 0 = q, 1 = k, 2 = v
+    int which = (int)(blockIdx.x % upr);   // 0 = q, 1 = k, 2 = v (absent tensors skipped)
+    if (!has_q) ++which;
     if (which == 1 && !has_k) ++which;
-    const int64_t row_step = nwaves / upr;
-    const int64_t row0 = wave / upr;
-
-    if (which == 2) {               // packed qkv: v += bias_v
-        for (int64_t r = row0; r < a.rows; r += row_step) {
-            T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
-            for (int64_t e0 = (int64_t)lane * E; e0 < HD; e0 += 64 * E) {
-                float vv[E], bv[E];
-                load_elems<T, E>(vr + e0, vv);
-                load_params<E>(a.bias_v + e0, bv);
+    const int64_t tile = blockIdx.x / upr;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r = tile * kTileWaves + wave;
+    const bool live = r < a.rows;
+    if (which == 2) {                      // packed qkv: v += bias_v (block-uniform branch)
+        if (!live) return;
+        T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
+        for (int e0 = lane * E; e0 < HD; e0 += 64 * E) {
+            float vv[E], bv[E];
+            load_elems<T, E>(vr + e0, vv);
+            load_params<E>(a.bias_v + e0, bv);
 #pragma unroll
-                for (int i = 0; i < E; ++i) vv[i] = add_rn(vv[i], bv[i]);
-                store_elems<T, E>(vr + e0, vv);
-            }
+            for (int i = 0; i < E; ++i) vv[i] = add_rn(vv[i], bv[i]);
+            store_elems<T, E>(vr + e0, vv);
         }
         return;
     }
     const T* __restrict__ in = static_cast<const T*>(which == 0 ? a.q_in : a.k_in);
     T* __restrict__ out = static_cast<T*>(which == 0 ? a.q_out : a.k_out);
+    const float* __restrict__ gamma = which == 0 ? a.gamma_q : a.gamma_k;
     const float* __restrict__ bias = which == 0 ? a.bias_q : a.bias_k;
-    const bool has_gamma = (which == 0 ? a.gamma_q : a.gamma_k) != nullptr;
-    const float* __restrict__ gsw = gs + which * NG * 4 * D;
+    const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
 
+    const int my_slot = lane % HALF;
+    const int my_axis = tab.axis[my_slot];
     const bool coord_pos = a.use_rope && a.phases == nullptr && a.coords != nullptr;
-    // The coordinate this lane's slot rotates by (pad slots: none) for row r,
-    // loaded one row ahead, so the phase math never waits on a load.
-    auto slot_coord = [&](int64_t r) -> float {
-        if (!coord_pos || r >= a.rows || my_axis < 0) return 0.0f;
-        return (float)a.coords[r * a.coord_cols + 1 + my_axis];
-    };
-    float cpos = slot_coord(row0);
-    for (int64_t r = row0; r < a.rows; r += row_step) {
-        const float npos = slot_coord(r + row_step);
-        float v[NG][E];
-#pragma unroll
-        for (int it = 0; it < NG; ++it) {
-            const int hh = 4 * it + g;
-#pragma unroll
-            for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
-            if (hh < H) load_elems<T, E, true>(in + r * a.in_stride + (int64_t)hh * D + m * E, v[it]);
-        }
+    float cpos = 0.0f;
+    if (live && coord_pos && my_axis >= 0) cpos = (float)a.coords[r * a.coord_cols + 1 + my_axis];
 
-        float pc[P], ps[P];
+    const int64_t rl = live ? r : a.rows - 1;   // dead waves load a valid row, store nothing
+    float v[NG][E];
+#pragma unroll
+    for (int it = 0; it < NG; ++it) {
+        const int hh = 4 * it + g;
+        const int hl = hh < H ? hh : H - 1;
+        load_elems<T, E, true>(in + rl * a.in_stride + (int64_t)hl * D + m * E, v[it]);
+    }
+
+    if (gamma != nullptr) {
+        for (int i = threadIdx.x; i < HD; i += kTileBlock) gs[i] = gamma[i] * a.rms_scale;
+    }
+
+    float pc[P], ps[P];
+    if (a.use_rope) {
+        if (a.phases != nullptr) {
+            const int64_t l = live ? r % a.phase_rows : 0;
+            float tmp[2 * P];
+            load_params<2 * P>(a.phases + (l * HALF + m * P) * 2, tmp);
+#pragma unroll
+            for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
+        } else {
+            float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};
+            if (!coord_pos) src.get(live ? r : 0, pos);
+            float c, s;
+            slot_phase(pos, my_axis, tab.freq[my_slot], c, s);
+#pragma unroll
+            for (int t = 0; t < P; ++t) {
+                pc[t] = lane_bcast(c, m * P + t);
+                ps[t] = lane_bcast(s, m * P + t);
+            }
+        }
+    }
+
+    if (gamma != nullptr) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS stores are done
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    if (!live) return;
+
+#pragma unroll
+    for (int it = 0; it < NG; ++it) {
+        const int hh = 4 * it + g;
+        const bool valid = hh < H;
+        if (bias != nullptr && valid) {
+            float bv[E];
+            load_params<E>(bias + (int64_t)hh * D + m * E, bv);
+#pragma unroll
+            for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
+        }
+        if (gamma != nullptr) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < E; ++i) ss += v[it][i] * v[it][i];
+            ss = row16_sum(ss);
+            const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+            float gv[E];
+            const float4* gp = reinterpret_cast<const float4*>(&gs[valid ? hh * D + m * E : 0]);
+#pragma unroll
+            for (int c4 = 0; c4 < E / 4; ++c4) {
+                const float4 w = gp[c4];
+                gv[4 * c4] = w.x; gv[4 * c4 + 1] = w.y; gv[4 * c4 + 2] = w.z; gv[4 * c4 + 3] = w.w;
+            }
+#pragma unroll
+            for (int i = 0; i < E; ++i) v[it][i] = (v[it][i] * rn) * gv[i];
+        }
         if (a.use_rope) {
-            if (a.phases != nullptr) {
-                const int64_t l = r % a.phase_rows;
-                float tmp[2 * P];  // P interleaved (cos, sin) pairs
-                load_params<2 * P>(a.phases + (l * HALF + m * P) * 2, tmp);
 #pragma unroll
-                for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
-            } else {
-                float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};   // this lane's slot axis only
-                if (!coord_pos) src.get(r, pos);
-                float c, s;
-                slot_phase(pos, my_axis, my_freq, c, s);
-#pragma unroll
-                for (int t = 0; t < P; ++t) {   // slot m*P + t lives in lane m*P + t
-                    pc[t] = lane_bcast(c, m * P + t);
-                    ps[t] = lane_bcast(s, m * P + t);
-                }
+            for (int t = 0; t < P; ++t) {
+                const float re = v[it][2 * t], im = v[it][2 * t + 1];
+                v[it][2 * t] = re * pc[t] - im * ps[t];
+                v[it][2 * t + 1] = re * ps[t] + im * pc[t];
             }
         }
-
-#pragma unroll
-        for (int it = 0; it < NG; ++it) {
-            const int hh = 4 * it + g;
-            const bool valid = hh < H;
-            if (bias != nullptr && valid) {
-                float bv[E];
-                load_params<E>(bias + (int64_t)hh * D + m * E, bv);
-#pragma unroll
-                for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
-            }
-            if (has_gamma) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int i = 0; i < E; ++i) ss += v[it][i] * v[it][i];
-                ss = row16_sum(ss);
-                // 1 / max(sqrt(ss), 1e-12): sqrt(ss) < 1e-12 <=> ss < 1e-24
-                const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
-                float gv[E];
-                const float4* gp = reinterpret_cast<const float4*>(&gsw[hh * D + m * E]);
-#pragma unroll
-                for (int c4 = 0; c4 < E / 4; ++c4) {
-                    const float4 w = gp[c4];
-                    gv[4 * c4] = w.x; gv[4 * c4 + 1] = w.y; gv[4 * c4 + 2] = w.z; gv[4 * c4 + 3] = w.w;
-                }
-#pragma unroll
-                for (int i = 0; i < E; ++i) v[it][i] = (v[it][i] * rn) * gv[i];
-            }
-            if (a.use_rope) {
-#pragma unroll
-                for (int t = 0; t < P; ++t) {
-                    const float re = v[it][2 * t], im = v[it][2 * t + 1];
-                    v[it][2 * t] = re * pc[t] - im * ps[t];
-                    v[it][2 * t + 1] = re * ps[t] + im * pc[t];
-                }
-            }
-            if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
-        }
-        cpos = npos;
+        if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
     }
 }
 
@@ -320,14 +305,9 @@ int resident_blocks(K kernel) {
 
 template <typename T, int D, int NG>
 hipError_t launch_fast(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
-    auto k = qk_rows_kernel<T, D, NG>;
-    static const int cap = resident_blocks(k);
     const int upr = (a.q_in != nullptr) + (a.k_in != nullptr) + (a.v != nullptr && a.bias_v != nullptr);
-    const int64_t need = (a.rows * upr + kWaves - 1) / kWaves;
-    int grid = (int)((T2H_QK_PERSIST && need > cap) ? cap : need);
-    // the kernel gives each wave one tensor: the wave count must be a multiple of upr
-    while ((grid * (int64_t)kWaves) % upr != 0) ++grid;
-    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, a, tab);
+    const int64_t tiles = (a.rows + kTileWaves - 1) / kTileWaves;
+    hipLaunchKernelGGL((qk_tile_kernel<T, D, NG>), dim3((unsigned)(tiles * upr)), dim3(kTileBlock), 0, s, a, tab);
     return hipGetLastError();
 }
 

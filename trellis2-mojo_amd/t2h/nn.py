@@ -105,11 +105,13 @@ class MultiHeadRMSNorm:
 
 def rope_freqs(head_dim: int, dim: int = 3, freq_lo: float = 1.0, freq_hi: float = 10000.0) -> np.ndarray:
     """freqs = freq_lo / freq_hi ** (arange(freq_dim) / freq_dim) in f32
-    (modules/rope.mojo:33-37)."""
-    fd = head_dim // 2 // dim
-    j = np.arange(fd, dtype=np.float32)
-    e = j / np.float32(fd)
-    return (np.float32(freq_lo) / np.power(np.float32(freq_hi), e)).astype(np.float32)
+    (modules/rope.mojo:33-37), computed by libt2h's host code with libm powf."""
+    out = np.zeros(max(head_dim // 2, 1), np.float32)
+    from ._lib import load, check
+    fd = load().t2h_rope_freqs(int(head_dim), int(dim), float(freq_lo), float(freq_hi), out.ctypes.data, out.size)
+    if fd < 0:
+        check(fd)
+    return out[:fd].copy()
 
 
 class RotaryPositionEmbedder:
