@@ -222,6 +222,39 @@ int32_t t2h_gate_residual_ln_modulate(
     int32_t cols, int32_t dtype, const int64_t* offsets, int32_t nbatch,
     int64_t rows_per_batch, void* stream);
 
+/* ---- resident-block glue over one const buffer ---------------------------
+ * The device-resident DiT cross block keeps its per-block glue constants in
+ * one f32 buffer `consts` of 12*C floats (gpu/block.mojo:255-289): pairs of
+ * [C] vectors at offsets 0, 2C, 4C, 6C, 8C, 10C =
+ *   (shift1, scale1) (self_out bias, gate1) (norm2 weight, bias)
+ *   (cross_out bias, 0) (shift3, scale3) (mlp2 bias, gate3).
+ * `off` selects a pair: consts[off : off+C] and consts[off+C : off+2C].
+ * All three calls take the reference kernels' arguments in their order, plus
+ * the storage dtype and the stream. eps is the blocks' 1e-6 (block.mojo:44). */
+
+/* Replaces: Metal ln_mod_rows (gpu/block.mojo:47-83). mode 1: dst =
+ * LN(x)*(1+consts[off+C+i]) + consts[off+i]; mode 2 (affine): dst =
+ * LN(x)*consts[off+i] + consts[off+C+i]. dst may alias x. */
+int32_t t2h_ln_mod_rows(const void* x, void* dst, const float* consts,
+                        int64_t rows, int32_t c, int32_t off, int32_t mode,
+                        int32_t dtype, void* stream);
+
+/* Replaces: Metal gate_add_bias_rows (gpu/block.mojo:86-110), in place:
+ * x += fl(h + consts[off+i]) * consts[off+C+i]   (use_gate 1)
+ * x += fl(h + consts[off+i])                     (use_gate 0). Bit-exact. */
+int32_t t2h_gate_add_bias_rows(void* x, const void* h, const float* consts,
+                               int64_t rows, int32_t c, int32_t off,
+                               int32_t use_gate, int32_t dtype, void* stream);
+
+/* Replaces the block's join + next norm pair, gate_add_bias_rows(join_off,
+ * use_gate) followed by ln_mod_rows(norm_off, mode) (gpu/block.mojo:324-349
+ * and 356-381), in one HBM pass: x updated in place, dst = the normed rows.
+ * dst must not alias x or h. */
+int32_t t2h_block_join_ln(void* x, const void* h, void* dst,
+                          const float* consts, int64_t rows, int32_t c,
+                          int32_t join_off, int32_t use_gate, int32_t norm_off,
+                          int32_t mode, int32_t dtype, void* stream);
+
 /* ---- timestep embedding --------------------------------------------------
  * Replaces TimestepEmbedder.timestep_embedding
  * (models/sparse_structure_flow.mojo:60-76): t [n] f32 -> out [n, dim]:

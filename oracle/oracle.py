@@ -369,3 +369,43 @@ def gate_residual(x, h, gate_rows, offsets=None, bias=None) -> np.ndarray:
             offsets = np.array([0, rows], np.int64)
         h = binop_rows(h, g, batch_broadcast_map(offsets), OP_MUL)
     return binop_flat(x, h, OP_ADD)
+
+
+def cross_block(x, m, norm2_w, norm2_b, self_attn, cross_attn, mlp, offsets=None, eps: float = 1e-6,
+                store=None) -> np.ndarray:
+    """Glue of the CPU cross block on feats [rows, C]: the order of
+    ModulatedSparseTransformerCrossBlock.forward (sparse/transformer/modulated.mojo:219-226)
+    and of the dense block (modules/transformer/modulated.mojo:186-200, _tail 192-200).
+    m: the six adaLN chunks [B, C]; the chains are numpy callables returning complete
+    outputs. `store` rounds a tensor to the storage type where the device path stores one."""
+    rnd = store or (lambda a: a)
+    x = _f32(x)
+    rows = x.shape[0]
+    if offsets is None:
+        offsets = np.array([0, rows], np.int64)
+    h = rnd(ln_modulate(x, m[0], m[1], offsets, eps))
+    h = rnd(_f32(self_attn(h)))
+    y = rnd(gate_residual(x, h, m[2], offsets))
+    h2 = rnd(layernorm(y, eps, affine=True, w=norm2_w, b=norm2_b))
+    h2 = rnd(_f32(cross_attn(h2)))
+    y = rnd(gate_residual(y, h2, None))
+    h3 = rnd(ln_modulate(y, m[3], m[4], offsets, eps))
+    h3 = rnd(_f32(mlp(h3)))
+    return rnd(gate_residual(y, h3, m[5], offsets))
+
+
+def cross_block_resident(x, bk, self_chain, cross_chain, mlp_chain, eps: float = 1e-6, store=None) -> np.ndarray:
+    """Glue of gpu_cross_block_enqueue (gpu/block.mojo:304-397) with the const
+    buffer bk [12C] (layout 255-289): the out-linear biases are folded into the
+    joins, the chains return their outputs without them."""
+    rnd = store or (lambda a: a)
+    x = _f32(x)
+    c = x.shape[1]
+    bk = _f32(bk).reshape(-1)
+    v = lambda k: bk[k * c:(k + 1) * c]
+    hs = rnd(ln_modulate(x, v(0), v(1), None, eps))                 # ln_mod_rows off 0, mode 1
+    x = rnd(gate_residual(x, rnd(_f32(self_chain(hs))), v(3), bias=v(2)))   # off 2C, gate
+    hs = rnd(layernorm(x, eps, affine=True, w=v(4), b=v(5)))        # off 4C, mode 2
+    x = rnd(gate_residual(x, rnd(_f32(cross_chain(hs))), None, bias=v(6)))  # off 6C, ungated
+    hs = rnd(ln_modulate(x, v(8), v(9), None, eps))                 # off 8C, mode 1
+    return rnd(gate_residual(x, rnd(_f32(mlp_chain(hs))), v(11), bias=v(10)))  # off 10C, gate

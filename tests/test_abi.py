@@ -57,6 +57,17 @@ def test_validation_without_device(lib):
     assert rc == _lib.T2H_EINVAL and b"needs phases, coords or grid_res" in lib.t2h_last_error()
     rc = lib.t2h_timestep_embedding(p, p, 4, 4096, 0, 10000.0, None)
     assert rc == _lib.T2H_EUNSUPPORTED
+    # resident-block glue: the reference kernels' mode / use_gate / offset domains
+    assert lib.t2h_ln_mod_rows(p, p, p, 4, 1536, 0, 0, 0, None) == _lib.T2H_EINVAL
+    assert b"bad mode 0" in lib.t2h_last_error()
+    assert lib.t2h_gate_add_bias_rows(p, p, p, 4, 1536, -1, 1, 0, None) == _lib.T2H_EINVAL
+    assert b"negative const offset" in lib.t2h_last_error()
+    assert lib.t2h_gate_add_bias_rows(p, p, p, 4, 1536, 0, 2, 0, None) == _lib.T2H_EINVAL
+    assert b"use_gate must be 0 or 1" in lib.t2h_last_error()
+    assert lib.t2h_block_join_ln(p, p, p, None, 4, 1536, 0, 1, 0, 1, 0, None) == _lib.T2H_EINVAL
+    assert b"NULL consts" in lib.t2h_last_error()
+    assert lib.t2h_block_join_ln(p, p, p, p, 4, 1536, 0, 1, 0, 3, 0, None) == _lib.T2H_EINVAL
+    assert b"bad mode 3" in lib.t2h_last_error()
 
 
 def test_empty_is_a_noop(lib):
@@ -64,6 +75,9 @@ def test_empty_is_a_noop(lib):
     assert lib.t2h_ln_modulate(None, None, 0, 1536, 0, 1e-6, 0, None, None, 0, None, 1, 0, None) == 0
     assert lib.t2h_activation(None, None, None, 0, 6144, 1, 3, None) == 0
     assert lib.t2h_gate_residual(None, None, None, None, None, 0, 0, 1536, 1, None, 1, 0, None) == 0
+    p = ctypes.c_void_p(16)
+    assert lib.t2h_gate_add_bias_rows(None, None, p, 0, 1536, 0, 1, 0, None) == 0
+    assert lib.t2h_block_join_ln(None, None, None, p, 0, 1536, 2 * 1536, 1, 4 * 1536, 2, 1, None) == 0
     assert lib.t2h_last_error() == b""
 
 

@@ -277,3 +277,80 @@ def test_f16_bf16_rounding_matches_torch():
                         np.array([65504, 65520, 65519.99, 1e-8, -0.0, np.inf], np.float32)]).astype(np.float32)
     assert np.array_equal(orc.round_f16(x), torch.from_numpy(x).half().float().numpy())
     assert np.array_equal(orc.round_bf16(x), torch.from_numpy(x).bfloat16().float().numpy())
+
+
+# ---- DiT cross-block glue: the two reference forms of one block ----------------
+def _block_case(seed, rows=64, c=48):
+    x = orc.randn(seed, (rows, c), std=2.0)
+    m = [orc.randn(seed + 1 + i, (1, c), std=0.3) for i in range(6)]
+    w2 = orc.randn(seed + 7, (c,), mean=1.0, std=0.2)
+    b2 = orc.randn(seed + 8, (c,), std=0.2)
+    biases = [orc.randn(seed + 9 + i, (c,), std=0.1) for i in range(3)]
+    return x, m, w2, b2, biases
+
+
+def _chains():
+    self_chain = lambda h: (np.roll(h, 1, axis=0) * np.float32(0.5)).astype(np.float32)
+    cross_chain = lambda h: (h[:, ::-1] * np.float32(-0.25)).astype(np.float32)
+    mlp_chain = lambda h: orc.activation(h, orc.ACT_GELU_TANH)
+    return self_chain, cross_chain, mlp_chain
+
+
+def _bk(m, w2, b2, biases):
+    c = w2.size
+    z = np.zeros(c, np.float32)
+    return np.concatenate([m[0].ravel(), m[1].ravel(), biases[0], m[2].ravel(), w2, b2, biases[1], z,
+                           m[3].ravel(), m[4].ravel(), biases[2], m[5].ravel()]).astype(np.float32)
+
+
+def test_block_resident_equals_cpu_order():
+    """gpu/block.mojo folds each out-linear bias into its residual join
+    (x + fl(h + bias) * gate); the CPU block adds it inside the chain
+    (x + fl(fl(h + bias) * gate)). Both are the same f32 sequence, so the
+    two restatements agree bit for bit, which pins the const-buffer pair
+    order (a swapped shift/scale or gate/bias pair fails)."""
+    x, m, w2, b2, biases = _block_case(900)
+    sc, cc, mc = _chains()
+    ab = lambda f, b: (lambda h: orc.add_bias(f(h), b))
+    cpu = orc.cross_block(x, m, w2, b2, ab(sc, biases[0]), ab(cc, biases[1]), ab(mc, biases[2]))
+    res = orc.cross_block_resident(x, _bk(m, w2, b2, biases), sc, cc, mc)
+    assert np.array_equal(cpu, res)
+    swapped = list(m)
+    swapped[0], swapped[1] = m[1], m[0]
+    assert not np.array_equal(orc.cross_block_resident(x, _bk(swapped, w2, b2, biases), sc, cc, mc), cpu)
+
+
+def test_block_closed_forms():
+    """Zero gates and a zero cross chain leave x unchanged; with gate1 = 1,
+    identity chains and zero shift/scale the self join is x + LN(x), checked
+    against float64."""
+    x, m, w2, b2, biases = _block_case(950)
+    c = x.shape[1]
+    zero = lambda h: np.zeros_like(h)
+    mz = [mm.copy() for mm in m]
+    mz[2][:] = 0
+    mz[5][:] = 0
+    out = orc.cross_block(x, mz, w2, b2, lambda h: h, zero, lambda h: h)
+    assert np.array_equal(out, x)
+    m1 = [np.zeros((1, c), np.float32) for _ in range(6)]
+    m1[2][:] = 1
+    out = orc.cross_block(x, m1, w2, b2, lambda h: h, zero, zero)
+    xd = x.astype(np.float64)
+    ln = (xd - xd.mean(1, keepdims=True)) / np.sqrt(xd.var(1, keepdims=True) + 1e-6)
+    assert np.max(np.abs(out - (xd + ln)) / np.maximum(np.abs(xd + ln), 1)) < 2e-6
+
+
+def test_pack_block_consts_layout():
+    """Host logic of t2h.block (torch CPU tensors): the const buffer follows
+    gpu/block.mojo:255-289, a missing out bias is zeros."""
+    from t2h import block
+
+    x, m, w2, b2, biases = _block_case(990, c=16)
+    bk = block.pack_block_consts([torch.from_numpy(mm) for mm in m], torch.from_numpy(w2), torch.from_numpy(b2),
+                                 *[torch.from_numpy(b) for b in biases])
+    assert np.array_equal(bk.numpy(), _bk(m, w2, b2, biases))
+    bk0 = block.pack_block_consts([torch.from_numpy(mm) for mm in m], torch.from_numpy(w2), torch.from_numpy(b2))
+    z = [np.zeros(16, np.float32)] * 3
+    assert np.array_equal(bk0.numpy(), _bk(m, w2, b2, z))
+    with pytest.raises(ValueError, match="expected 6 mod chunks"):
+        block.pack_block_consts([torch.from_numpy(mm) for mm in m[:5]], torch.from_numpy(w2), torch.from_numpy(b2))

@@ -472,6 +472,51 @@ int32_t t2h_modulation_add(const float* mod, const float* modulation, float* m, 
     return hip_status(launch_modulation_add(mod, modulation, m, n, width, static_cast<hipStream_t>(stream)), fn);
 }
 
+// Resident-block glue over one const buffer: the pair at `off` is
+// consts[off : off+c], consts[off+c : off+2c] (gpu/block.mojo:255-289).
+static constexpr float kBlockEps = 1e-6f;   // gpu/block.mojo:44
+
+static int32_t check_pair(const float* consts, int64_t rows, int32_t c, int32_t off, const char* fn) {
+    if (rows < 0 || c <= 0) return fail(T2H_EINVAL, "%s: bad shape [%lld, %d]", fn, (long long)rows, c);
+    if (off < 0) return fail(T2H_EINVAL, "%s: negative const offset %d", fn, off);
+    if (consts == nullptr) return fail(T2H_EINVAL, "%s: NULL consts", fn);
+    return T2H_OK;
+}
+
+int32_t t2h_ln_mod_rows(const void* x, void* dst, const float* consts, int64_t rows, int32_t c, int32_t off,
+                        int32_t mode, int32_t dtype, void* stream) {
+    const char* fn = "t2h_ln_mod_rows";
+    if (int32_t rc = check_pair(consts, rows, c, off, fn)) return rc;
+    if (mode != T2H_LN_MODULATE && mode != T2H_LN_AFFINE) return fail(T2H_EINVAL, "%s: bad mode %d", fn, mode);
+    const float* a = consts + off;
+    return t2h_ln_modulate(x, dst, rows, c, dtype, kBlockEps, mode, a, a + c, 0, nullptr, 1, 0, stream);
+}
+
+int32_t t2h_gate_add_bias_rows(void* x, const void* h, const float* consts, int64_t rows, int32_t c, int32_t off,
+                               int32_t use_gate, int32_t dtype, void* stream) {
+    const char* fn = "t2h_gate_add_bias_rows";
+    if (int32_t rc = check_pair(consts, rows, c, off, fn)) return rc;
+    if (use_gate != 0 && use_gate != 1) return fail(T2H_EINVAL, "%s: use_gate must be 0 or 1", fn);
+    if (rows > 0 && x == nullptr) return fail(T2H_EINVAL, "%s: NULL x", fn);
+    const float* a = consts + off;
+    return t2h_gate_residual(x, h, x, a, use_gate ? a + c : nullptr, 0, rows, c, dtype, nullptr, 1, 0, stream);
+}
+
+int32_t t2h_block_join_ln(void* x, const void* h, void* dst, const float* consts, int64_t rows, int32_t c,
+                          int32_t join_off, int32_t use_gate, int32_t norm_off, int32_t mode, int32_t dtype,
+                          void* stream) {
+    const char* fn = "t2h_block_join_ln";
+    if (int32_t rc = check_pair(consts, rows, c, join_off, fn)) return rc;
+    if (norm_off < 0) return fail(T2H_EINVAL, "%s: negative const offset %d", fn, norm_off);
+    if (use_gate != 0 && use_gate != 1) return fail(T2H_EINVAL, "%s: use_gate must be 0 or 1", fn);
+    if (mode != T2H_LN_MODULATE && mode != T2H_LN_AFFINE) return fail(T2H_EINVAL, "%s: bad mode %d", fn, mode);
+    if (rows > 0 && (dst == x || dst == h)) return fail(T2H_EINVAL, "%s: dst must not alias x or h", fn);
+    const float* j = consts + join_off;
+    const float* n = consts + norm_off;
+    return t2h_gate_residual_ln_modulate(x, h, x, dst, j, use_gate ? j + c : nullptr, 0, kBlockEps, mode, n, n + c, 0,
+                                         rows, c, dtype, nullptr, 1, 0, stream);
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

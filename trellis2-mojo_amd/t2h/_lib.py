@@ -43,6 +43,9 @@ _SIGNATURES = {
     "t2h_timestep_embedding": [c_p, c_p, c_i64, c_i32, c_i32, c_f64, c_p],
     "t2h_coords_to_offsets": [c_p, c_i64, c_i32, c_i32, c_p, c_p, c_p],
     "t2h_modulation_add": [c_p, c_p, c_p, c_i64, c_i64, c_p],
+    "t2h_ln_mod_rows": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p],
+    "t2h_gate_add_bias_rows": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p],
+    "t2h_block_join_ln": [c_p, c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_p],
     "t2h_h_ln_modulate": [c_p, c_p, c_i64, c_i32, c_f32, c_i32, c_p, c_p, c_p, c_i32, c_i64],
     "t2h_h_qk_rmsnorm_rope": [c_p, c_p, c_p, c_p, c_i64, c_i32, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_i32, c_p,
                               c_i64, c_p, c_i32, c_i32],

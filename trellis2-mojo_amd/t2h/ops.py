@@ -353,6 +353,54 @@ def modulation_add(mod, modulation) -> torch.Tensor:
     return out
 
 
+# ---- resident-block glue over one const buffer ----------------------------------
+def _block_consts(consts, c: int, offs, what: str) -> int:
+    _dev(consts, what)
+    if consts.dtype != torch.float32 or not consts.is_contiguous():
+        raise ValueError(f"{what}: consts must be contiguous float32")
+    for off in offs:
+        if off < 0 or off + 2 * c > consts.numel():
+            raise ValueError(f"{what}: const pair at {off} outside a buffer of {consts.numel()} floats")
+    return consts.data_ptr()
+
+
+def _same_rows(x, h, what: str):
+    rows, c = _rows_view(x, what)
+    if h.shape != x.shape or h.dtype != x.dtype or not h.is_contiguous():
+        raise ValueError(f"{what}: tensors must match x")
+    return rows, c
+
+
+def ln_mod_rows(x, dst, consts, off: int, mode: int) -> torch.Tensor:
+    """Metal ln_mod_rows: dst = LN(x) with the const pair at `off` (mode 1
+    modulate, mode 2 affine), eps 1e-6."""
+    rows, c = _same_rows(x, dst, "ln_mod_rows")
+    cp = _block_consts(consts, c, [off], "ln_mod_rows")
+    call("t2h_ln_mod_rows", x.data_ptr(), dst.data_ptr(), cp, rows, c, int(off), int(mode), _dtype(x, "ln_mod_rows"),
+         _stream())
+    return dst
+
+
+def gate_add_bias_rows(x, h, consts, off: int, use_gate: int) -> torch.Tensor:
+    """Metal gate_add_bias_rows, in place: x += (h + bias) [* gate]."""
+    rows, c = _same_rows(x, h, "gate_add_bias_rows")
+    cp = _block_consts(consts, c, [off], "gate_add_bias_rows")
+    call("t2h_gate_add_bias_rows", x.data_ptr(), h.data_ptr(), cp, rows, c, int(off), int(use_gate),
+         _dtype(x, "gate_add_bias_rows"), _stream())
+    return x
+
+
+def block_join_ln(x, h, dst, consts, join_off: int, use_gate: int, norm_off: int, mode: int) -> torch.Tensor:
+    """gate_add_bias_rows(join_off) then ln_mod_rows(norm_off) in one pass;
+    x updated in place, dst = the normed rows."""
+    rows, c = _same_rows(x, h, "block_join_ln")
+    _same_rows(x, dst, "block_join_ln")
+    cp = _block_consts(consts, c, [join_off, norm_off], "block_join_ln")
+    call("t2h_block_join_ln", x.data_ptr(), h.data_ptr(), dst.data_ptr(), cp, rows, c, int(join_off), int(use_gate),
+         int(norm_off), int(mode), _dtype(x, "block_join_ln"), _stream())
+    return dst
+
+
 def device_init(device: int = 0) -> None:
     call("t2h_device_init", int(device))
 
