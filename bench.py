@@ -249,6 +249,46 @@ def other_configs(torch, dev):
     return res
 
 
+def next_rows(torch, dev, chain, reps):
+    """The per-token work around the chain, on the config-5 rows (f16): the
+    block glue over one const buffer (chains stubbed by a resident tensor, so
+    only the glue kernels run) and the attention epilogue + head-major pack."""
+    from t2h import block, ops
+
+    T, C, H, D = chain.T, chain.C, chain.H, chain.D
+    e = 2
+    res = {}
+
+    def rec(name, fn, nbytes):
+        fn()
+        ms = time_region(torch, fn, reps) / reps
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                     "pct_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 2)}
+        log(f"  {name:<26s} {ms*1e3:8.1f} us  {nbytes/ms/1e6:8.1f} GB/s ({nbytes/ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
+
+    m = [chain.shift, chain.scale, chain.gate, chain.shift, chain.scale, chain.gate]
+    ones = torch.ones(C, dtype=torch.float32, device=dev)
+    bk = block.pack_block_consts(m, ones, chain.shift.reshape(-1), chain.bias[:C], chain.bias[C:2 * C],
+                                 chain.bias[2 * C:3 * C])
+    xs = chain.x.clone()
+    hres = chain.y
+    stub = lambda h: hres
+    for fused, nrows in ((True, 13), (False, 15)):   # row-passes of C elements per block
+        rec(f"block_glue_{'fused' if fused else 'unfused'}",
+            lambda f=fused: block.cross_block_enqueue(xs, bk, stub, stub, stub, fused=f), nrows * T * C * e)
+    del xs
+    mp = (T + 63) // 64 * 64
+    qkv = chain.u[:, :3 * C].contiguous()
+    q3 = qkv.reshape(T, 3, H, D)
+    b3 = chain.bias[:3 * C].reshape(3, H * D)
+    rec("attn_pack_qkv_to_heads", lambda: ops.attn_pack(q3[:, 0], q3[:, 1], q3[:, 2], mp=mp, lp=mp, bias_q=b3[0],
+                                                        bias_k=b3[1], bias_v=b3[2], gamma_q=chain.gq,
+                                                        gamma_k=chain.gk, freqs=chain.freqs, coords=chain.coords),
+        T * 3 * C * e + 3 * mp * C * e + T * 16)
+    del qkv, q3
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -312,6 +352,8 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(chain, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']:.0f} tokens/s on {cpu['cores']} threads ({cpu['sample']})")
+    log("next rows on the config-5 rows (f16):")
+    extra = next_rows(torch, dev, chain, max(10, args.steps))
     if args.all_configs:
         log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
         other = other_configs(torch, dev)
@@ -330,6 +372,7 @@ def main():
                    "tokens": chain.T, "width": 1536, "heads": 12, "head_dim": 128, "hidden": 6144,
                    "grid": "128^3 thickened sphere shell", "bytes_per_token": 52240},
         "per_op": {k: {"us": round(v["us"], 2), "gbs": round(v["gbs"], 1)} for k, v in per_op.items()},
+        "next_rows": extra,
         "roofline": roofline,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
     }

@@ -169,6 +169,34 @@ int32_t t2h_qkv_bias_rmsnorm_rope(void* qkv, int64_t rows, int32_t heads,
                                   int32_t coord_cols, int32_t grid_res,
                                   void* stream);
 
+/* ---- attention epilogue + head-major packing ------------------------------
+ * Replaces the self-attention chain's bias_rms_rope_qkv followed by pack_q_z
+ * and pack_kv_z (gpu/attention.mojo:507-563, 566-594, 634-662; sequence
+ * 987-1013), and the cross chain's bias_rms_q + pack_q_z (596-631,
+ * 1223-1234), in one pass that leaves q/k/v unmodified:
+ *   q, k, v: [rows, H, D] rows in_stride elements apart (0 = H*D); views of a
+ *            packed qkv [rows, 3, H, D] use in_stride 3*H*D. NULL = absent.
+ *   q, k: + bias, RMS (gamma_q/gamma_k, both or none; n = max(|x|, 1e-12),
+ *         x / n * gamma * sqrt(f32(D))), RoPE (positions as in
+ *         t2h_qk_rmsnorm_rope); v: + bias only.
+ *   qh    [H, mp, D] = q * (1 / sqrt(f32(D)))           (NULL = skip)
+ *   k_out [H, D, lp] (k_transposed = 1, the reference's kt; lp % 8 == 0)
+ *         or [H, lp, D] (k_transposed = 0)               (NULL = skip)
+ *   vh    [H, lp, D]                                     (NULL = skip)
+ * Rows rows..mp-1 of qh and rows..lp-1 of k_out / vh are written as zeros.
+ * head_dim 64 or 128. Outputs must not overlap the inputs. */
+int32_t t2h_attn_pack(const void* q, const void* k, const void* v,
+                      int64_t in_stride, int64_t rows, int32_t heads,
+                      int32_t head_dim, int32_t dtype, const float* bias_q,
+                      const float* bias_k, const float* bias_v,
+                      const float* gamma_q, const float* gamma_k,
+                      int32_t use_rope, const float* freqs_host,
+                      int32_t freq_dim, int32_t pos_dim, const float* phases,
+                      int64_t phase_rows, const int32_t* coords,
+                      int32_t coord_cols, int32_t grid_res, void* qh,
+                      int64_t mp, void* k_out, void* vh, int64_t lp,
+                      int32_t k_transposed, void* stream);
+
 /* Host function (no device work): the embedders' frequency table
  * freqs[j] = f32(freq_lo) / f32(freq_hi) ** (f32(j) / f32(freq_dim)),
  * freq_dim = head_dim / 2 / dim, in f32 with libm powf — the constructor of

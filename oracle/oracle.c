@@ -420,6 +420,41 @@ void orc_gate(const float* x, const float* g, float* out, int64_t n, int64_t l, 
 }
 
 /* ------------------------------------------------------------------------ */
+/* pack_q_z / pack_kv_z: gpu/attention.mojo:566-594, 634-662                 */
+/* ------------------------------------------------------------------------ */
+void orc_pack_q(const float* qkv, float* qh, int64_t l, int64_t h, int64_t d, int64_t mp, int64_t stride) {
+    const float scale = 1.0f / sqrtf((float)d); /* attention.mojo:587 */
+    for (int64_t z = 0; z < h; ++z)
+        for (int64_t t = 0; t < mp; ++t) {
+            float* dst = qh + (z * mp + t) * d;
+            if (t < l) {
+                const float* src = qkv + t * stride + z * d;
+                for (int64_t e = 0; e < d; ++e) dst[e] = src[e] * scale;
+            } else {
+                for (int64_t e = 0; e < d; ++e) dst[e] = 0.0f;
+            }
+        }
+}
+
+void orc_pack_kv(const float* qkv, float* kt, float* vh, int64_t l, int64_t h, int64_t d, int64_t lp) {
+    const int64_t hd = h * d;
+    for (int64_t z = 0; z < h; ++z)
+        for (int64_t t = 0; t < lp; ++t) {
+            const int64_t kb = z * d * lp;
+            float* vdst = vh + (z * lp + t) * d;
+            for (int64_t e = 0; e < d; ++e) {
+                if (t < l) { /* attention.mojo:652-656 */
+                    kt[kb + e * lp + t] = qkv[t * 3 * hd + hd + z * d + e];
+                    vdst[e] = qkv[t * 3 * hd + 2 * hd + z * d + e];
+                } else {
+                    kt[kb + e * lp + t] = 0.0f;
+                    vdst[e] = 0.0f;
+                }
+            }
+        }
+}
+
+/* ------------------------------------------------------------------------ */
 /* TimestepEmbedder.timestep_embedding: models/sparse_structure_flow.mojo:60-76 */
 /* ------------------------------------------------------------------------ */
 void orc_timestep_embedding(const float* t, int64_t n, int64_t dim,

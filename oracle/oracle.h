@@ -118,6 +118,16 @@ void orc_add_bias(const float* x, const float* bias, float* out,
 void orc_gate(const float* x, const float* g, float* out,
               int64_t n, int64_t l, int64_t c);
 
+/* ---- head-major attention packs: gpu/attention.mojo:566-594, 634-662 -- */
+/* qh [h, mp, d] = q rows (`stride` apart, head z at z*d) * 1/sqrt(f32(d));
+ * rows l..mp-1 zero. */
+void orc_pack_q(const float* qkv, float* qh, int64_t l, int64_t h, int64_t d,
+                int64_t mp, int64_t stride);
+/* qkv [l, 3, h, d] parts 1/2 -> kt [h, d, lp] (transposed) and vh [h, lp, d];
+ * pad columns / rows l..lp-1 zero. */
+void orc_pack_kv(const float* qkv, float* kt, float* vh, int64_t l, int64_t h,
+                 int64_t d, int64_t lp);
+
 /* ---- TimestepEmbedder.timestep_embedding: sparse_structure_flow.mojo:60-76 */
 void orc_timestep_embedding(const float* t, int64_t n, int64_t dim,
                             double max_period, float* out /* [n, dim] */);

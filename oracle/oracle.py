@@ -409,3 +409,46 @@ def cross_block_resident(x, bk, self_chain, cross_chain, mlp_chain, eps: float =
     x = rnd(gate_residual(x, rnd(_f32(cross_chain(hs))), None, bias=v(6)))  # off 6C, ungated
     hs = rnd(ln_modulate(x, v(8), v(9), None, eps))                 # off 8C, mode 1
     return rnd(gate_residual(x, rnd(_f32(mlp_chain(hs))), v(11), bias=v(10)))  # off 10C, gate
+
+
+def pack_q(q, l: int, h: int, d: int, mp: int, stride: int) -> np.ndarray:
+    """pack_q_z (gpu/attention.mojo:566-594): q rows `stride` apart -> qh
+    [h, mp, d] scaled by 1/sqrt(f32(d)), pad rows zero."""
+    q = _f32(q).reshape(-1)
+    out = np.empty((h, mp, d), np.float32)
+    lib().orc_pack_q(_p(q), _p(out), _i64(l), _i64(h), _i64(d), _i64(mp), _i64(stride))
+    return out
+
+
+def pack_kv(qkv, l: int, h: int, d: int, lp: int):
+    """pack_kv_z (gpu/attention.mojo:634-662): qkv [l, 3, h, d] -> kt [h, d, lp]
+    (transposed) and vh [h, lp, d], pads zero."""
+    qkv = _f32(qkv).reshape(-1)
+    kt = np.empty((h, d, lp), np.float32)
+    vh = np.empty((h, lp, d), np.float32)
+    lib().orc_pack_kv(_p(qkv), _p(kt), _p(vh), _i64(l), _i64(h), _i64(d), _i64(lp))
+    return kt, vh
+
+
+def bias_rms_rope_qkv(qkv, h: int, d: int, bias, gamma_q, gamma_k, phases, use_rms: bool = True,
+                      use_rope: bool = True) -> np.ndarray:
+    """bias_rms_rope_qkv (gpu/attention.mojo:507-563) on qkv [rows, 3, h, d]:
+    + bias [3hd] on q, k and v, then RMS-normalise and rotate q and k."""
+    qkv = _f32(qkv).reshape(-1, 3, h, d)
+    if bias is not None:
+        qkv = (qkv + _f32(bias).reshape(3, h, d)).astype(np.float32)
+    q, k = qk_rms_rope(qkv[:, 0], qkv[:, 1], gamma_q, gamma_k, phases, use_rms=use_rms, use_rope=use_rope)
+    return np.stack([q, k, qkv[:, 2]], axis=1).astype(np.float32)
+
+
+def attn_pack(qkv, h: int, d: int, mp: int, lp: int, bias=None, gamma_q=None, gamma_k=None, phases=None):
+    """The self-attention chain's epilogue: bias_rms_rope_qkv, pack_q_z and
+    pack_kv_z in the order of gpu/attention.mojo:987-1013, all in f32.
+    Returns (qh, kt, vh)."""
+    rows = _f32(qkv).reshape(-1, 3 * h * d).shape[0]
+    e = bias_rms_rope_qkv(qkv, h, d, bias, gamma_q, gamma_k, phases, use_rms=gamma_q is not None,
+                          use_rope=phases is not None)
+    e = e.reshape(rows, 3 * h * d)
+    qh = pack_q(e, rows, h, d, mp, 3 * h * d)
+    kt, vh = pack_kv(e, rows, h, d, lp)
+    return qh, kt, vh

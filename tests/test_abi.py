@@ -68,6 +68,16 @@ def test_validation_without_device(lib):
     assert b"NULL consts" in lib.t2h_last_error()
     assert lib.t2h_block_join_ln(p, p, p, p, 4, 1536, 0, 1, 0, 3, 0, None) == _lib.T2H_EINVAL
     assert b"bad mode 3" in lib.t2h_last_error()
+    # attention pack: shape, padding and layout domains
+    rc = lib.t2h_attn_pack(p, p, p, 0, 8, 4, 96, 0, None, None, None, None, None, 0, None, 0, 3, None, 0, None, 0,
+                           0, p, 8, p, p, 8, 1, None)
+    assert rc == _lib.T2H_EUNSUPPORTED and b"head_dim must be 64 or 128" in lib.t2h_last_error()
+    rc = lib.t2h_attn_pack(p, p, p, 0, 8, 4, 128, 0, None, None, None, None, None, 0, None, 0, 3, None, 0, None, 0,
+                           0, p, 4, None, None, 0, 1, None)
+    assert rc == _lib.T2H_EINVAL and b"mp < rows" in lib.t2h_last_error()
+    rc = lib.t2h_attn_pack(p, p, p, 0, 8, 4, 128, 0, None, None, None, None, None, 0, None, 0, 3, None, 0, None, 0,
+                           0, None, 0, p, None, 12, 1, None)
+    assert rc == _lib.T2H_EINVAL and b"lp % 8 == 0" in lib.t2h_last_error()
 
 
 def test_empty_is_a_noop(lib):

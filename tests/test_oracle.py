@@ -354,3 +354,27 @@ def test_pack_block_consts_layout():
     assert np.array_equal(bk0.numpy(), _bk(m, w2, b2, z))
     with pytest.raises(ValueError, match="expected 6 mod chunks"):
         block.pack_block_consts([torch.from_numpy(mm) for mm in m[:5]], torch.from_numpy(w2), torch.from_numpy(b2))
+
+
+# ---- head-major attention packs: gpu/attention.mojo:566-594, 634-662 -----------
+def test_packs_are_numpy_transposes():
+    """pack_q_z / pack_kv_z restated, checked against numpy's own reshapes:
+    qh[z, t] = q[t, z] * f32(1/sqrt(d)) (one f32 product), kt[z, e, t] =
+    k[t, z, e], vh[z, t] = v[t, z], pads zero. A transposed kt (the
+    [h, lp, d] layout) or a missing scale fails."""
+    l, h, d, lp = 37, 3, 16, 64
+    qkv = orc.randn(77, (l, 3, h, d))
+    qh = orc.pack_q(qkv.reshape(l, -1), l, h, d, lp, 3 * h * d)
+    kt, vh = orc.pack_kv(qkv, l, h, d, lp)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    want_q = np.zeros((h, lp, d), np.float32)
+    want_q[:, :l] = (qkv[:, 0] * scale).transpose(1, 0, 2)
+    want_k = np.zeros((h, d, lp), np.float32)
+    want_k[:, :, :l] = qkv[:, 1].transpose(1, 2, 0)
+    want_v = np.zeros((h, lp, d), np.float32)
+    want_v[:, :l] = qkv[:, 2].transpose(1, 0, 2)
+    assert np.array_equal(qh, want_q) and np.array_equal(kt, want_k) and np.array_equal(vh, want_v)
+    assert not np.array_equal(kt, want_v.transpose(0, 2, 1))
+    # cross-chain stride (q alone, rows h*d apart)
+    q = orc.randn(78, (l, h, d))
+    assert np.array_equal(orc.pack_q(q.reshape(l, -1), l, h, d, l, h * d)[:, :l], (q * scale).transpose(1, 0, 2))

@@ -346,6 +346,81 @@ int32_t t2h_qkv_bias_rmsnorm_rope(void* qkv, int64_t rows, int32_t heads, int32_
                      freqs_host, freq_dim, pos_dim, phases, phase_rows, coords, coord_cols, grid_res, stream, fn);
 }
 
+static bool aligned(const void* p, int64_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+int32_t t2h_attn_pack(const void* q, const void* k, const void* v, int64_t in_stride, int64_t rows, int32_t heads,
+                      int32_t head_dim, int32_t dtype, const float* bias_q, const float* bias_k, const float* bias_v,
+                      const float* gamma_q, const float* gamma_k, int32_t use_rope, const float* freqs_host,
+                      int32_t freq_dim, int32_t pos_dim, const float* phases, int64_t phase_rows,
+                      const int32_t* coords, int32_t coord_cols, int32_t grid_res, void* qh, int64_t mp, void* k_out,
+                      void* vh, int64_t lp, int32_t k_transposed, void* stream) {
+    const char* fn = "t2h_attn_pack";
+    if (!dtype_ok(dtype)) return fail(T2H_EINVAL, "%s: bad dtype %d", fn, dtype);
+    if (rows < 0 || heads <= 0 || heads > 65535) return fail(T2H_EINVAL, "%s: bad shape", fn);
+    if (head_dim != 64 && head_dim != 128) return fail(T2H_EUNSUPPORTED, "%s: head_dim must be 64 or 128", fn);
+    const int64_t hd = (int64_t)heads * head_dim;
+    if (in_stride == 0) in_stride = hd;
+    if (in_stride < hd) return fail(T2H_EINVAL, "%s: row stride < heads * head_dim", fn);
+    if (qh == nullptr && k_out == nullptr && vh == nullptr) return fail(T2H_EINVAL, "%s: no output", fn);
+    if (rows > 0 && ((qh != nullptr && q == nullptr) || (k_out != nullptr && k == nullptr) ||
+                     (vh != nullptr && v == nullptr)))
+        return fail(T2H_EINVAL, "%s: an output needs its input tensor", fn);
+    if (qh != nullptr && mp < rows) return fail(T2H_EINVAL, "%s: mp < rows", fn);
+    if ((k_out != nullptr || vh != nullptr) && lp < rows) return fail(T2H_EINVAL, "%s: lp < rows", fn);
+    if (k_out != nullptr && k_transposed && lp % 8 != 0) return fail(T2H_EINVAL, "%s: transposed k needs lp %% 8 == 0", fn);
+    if (qh == nullptr) mp = 0;
+    if (k_out == nullptr && vh == nullptr) lp = 0;
+    if (qh != nullptr && k_out != nullptr && (gamma_q == nullptr) != (gamma_k == nullptr))
+        return fail(T2H_EINVAL, "%s: gamma_q and gamma_k must both be given or both NULL", fn);
+    RopeSlots tab;
+    std::memset(&tab, 0, sizeof(tab));
+    if (use_rope && (qh != nullptr || k_out != nullptr)) {
+        if (int32_t rc = build_slots(head_dim, freqs_host, freq_dim, pos_dim, tab, fn)) return rc;
+        if (int32_t rc = check_positions(phases, phase_rows, coords, coord_cols, grid_res, pos_dim, fn)) return rc;
+    } else {
+        use_rope = 0;
+    }
+    // each lane moves head_dim/16 elements: min(16, that many bytes) alignment
+    const int64_t es = dtype == T2H_F32 ? 4 : 2;
+    const int64_t chunk = (head_dim / 16) * es < 16 ? (head_dim / 16) * es : 16;
+    if ((in_stride * es) % chunk != 0 || !aligned(q, chunk) || !aligned(k, chunk) || !aligned(v, chunk))
+        return fail(T2H_EINVAL, "%s: inputs must be %lld-byte aligned", fn, (long long)chunk);
+    if (!aligned(qh, 16) || !aligned(k_out, 16) || !aligned(vh, 16) || !aligned(bias_q, 16) || !aligned(bias_k, 16) ||
+        !aligned(bias_v, 16) || !aligned(gamma_q, 16) || !aligned(gamma_k, 16) || !aligned(phases, 16))
+        return fail(T2H_EINVAL, "%s: outputs and f32 parameters must be 16-byte aligned", fn);
+    if (mp == 0 && lp == 0) return ok();
+    PackArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.rows = rows;
+    a.in_stride = in_stride;
+    a.heads = heads;
+    a.head_dim = head_dim;
+    a.dtype = dtype;
+    a.bias_q = bias_q;
+    a.bias_k = bias_k;
+    a.bias_v = bias_v;
+    a.gamma_q = gamma_q;
+    a.gamma_k = gamma_k;
+    a.rms_scale = std::sqrt((float)head_dim);           // sqrt(Float32(d)), attention.mojo:539
+    a.q_scale = 1.0f / std::sqrt((float)head_dim);      // attention.mojo:587
+    a.use_rope = use_rope ? 1 : 0;
+    a.pos_dim = pos_dim;
+    a.phases = use_rope ? phases : nullptr;
+    a.phase_rows = phase_rows;
+    a.coords = (use_rope && phases == nullptr) ? coords : nullptr;
+    a.coord_cols = coord_cols;
+    a.grid_res = grid_res;
+    a.qh = qh;
+    a.mp = mp;
+    a.k_out = k_out;
+    a.vh = vh;
+    a.lp = lp;
+    a.k_transposed = k_transposed ? 1 : 0;
+    return hip_status(launch_pack(a, tab, static_cast<hipStream_t>(stream)), fn);
+}
+
 int32_t t2h_rope_freqs(int32_t head_dim, int32_t dim, double freq_lo, double freq_hi, float* freqs_host,
                        int32_t capacity) {
     if (head_dim <= 0 || head_dim % 2 != 0)

@@ -70,6 +70,38 @@ struct QkArgs {
     int32_t grid_res;        // position source 3
 };
 
+// Self-attention epilogue + head-major packing (t2h_attn_pack).
+struct PackArgs {
+    const void* q;           // [rows, H, D] rows in_stride apart; any may be nullptr
+    const void* k;
+    const void* v;
+    int64_t rows;
+    int64_t in_stride;
+    int32_t heads;
+    int32_t head_dim;
+    int32_t dtype;
+    const float* bias_q;
+    const float* bias_k;
+    const float* bias_v;
+    const float* gamma_q;    // nullptr = no RMS
+    const float* gamma_k;
+    float rms_scale;         // f32 sqrt(head_dim)
+    float q_scale;           // 1 / f32 sqrt(head_dim), baked into qh
+    int32_t use_rope;
+    int32_t pos_dim;
+    const float* phases;
+    int64_t phase_rows;
+    const int32_t* coords;
+    int32_t coord_cols;
+    int32_t grid_res;
+    void* qh;                // [H, mp, D]
+    int64_t mp;
+    void* k_out;             // [H, D, lp] (k_transposed) or [H, lp, D]
+    void* vh;                // [H, lp, D]
+    int64_t lp;
+    int32_t k_transposed;
+};
+
 struct PhaseArgs {
     float* out;
     int64_t rows;
@@ -102,6 +134,7 @@ hipError_t launch_ln(const LnArgs& a, hipStream_t s);
 // t2h_qk.hip
 hipError_t launch_qk(const QkArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_phases(const PhaseArgs& a, const RopeSlots& tab, hipStream_t s);
+hipError_t launch_pack(const PackArgs& a, const RopeSlots& tab, hipStream_t s);
 // t2h_eltwise.hip
 hipError_t launch_activation(const EltArgs& a, hipStream_t s);
 hipError_t launch_gate_residual(const EltArgs& a, hipStream_t s);

@@ -1,0 +1,51 @@
+// Device helpers of the in-kernel RoPE: token positions from int voxel coords
+// or the dense grid index, and the cos/sin of one rotary slot.
+// Reference: sparse/attention/rope.mojo:48-66 (angle = f32(coord) * freq),
+// models/sparse_structure_flow.mojo:132-151 (dense 'ij' grid),
+// modules/rope.mojo:51-60 (axis-major slots, identity pad slots).
+#pragma once
+#include "t2h_device.h"
+
+namespace t2h {
+namespace {
+
+// Position of token row r along `axis` (f32, exact for |coord| < 2^24).
+struct PosSource {
+    const int32_t* coords;
+    int32_t coord_cols;
+    int32_t grid_res;
+    int32_t pos_dim;
+    __device__ __forceinline__ void get(int64_t r, float* pos) const {
+        if (coords != nullptr) {
+            const int32_t* cr = coords + r * (int64_t)coord_cols + 1;
+#pragma unroll
+            for (int ax = 0; ax < T2H_MAX_POS_DIM; ++ax) pos[ax] = ax < pos_dim ? (float)cr[ax] : 0.0f;
+        } else {
+            const int64_t R = grid_res;
+            const int64_t l = r % (R * R * R);
+            pos[0] = (float)(l / (R * R));
+            pos[1] = (float)((l / R) % R);
+            pos[2] = (float)(l % R);
+            pos[3] = 0.0f;
+        }
+    }
+};
+
+__device__ __forceinline__ float pick_axis(const float* pos, int ax) {
+    return ax == 0 ? pos[0] : ax == 1 ? pos[1] : ax == 2 ? pos[2] : pos[3];
+}
+
+// cos/sin of one slot: angle = pos[axis] * freq rounded to f32, then accurate
+// (full-range reduced) cosf/sinf; identity for pad slots (axis < 0).
+__device__ __forceinline__ void slot_phase(const float* pos, int ax, float freq, float& c, float& s) {
+    if (ax < 0) {
+        c = 1.0f;
+        s = 0.0f;
+    } else {
+        const float angle = __fmul_rn(pick_axis(pos, ax), freq);
+        sincosf(angle, &s, &c);
+    }
+}
+
+}  // namespace
+}  // namespace t2h

@@ -34,6 +34,8 @@ _SIGNATURES = {
                             c_i32, c_p, c_i32, c_i32, c_p, c_i64, c_p, c_i32, c_i32, c_p],
     "t2h_qkv_bias_rmsnorm_rope": [c_p, c_i64, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_i32, c_p, c_i32, c_i32, c_p,
                                   c_i64, c_p, c_i32, c_i32, c_p],
+    "t2h_attn_pack": [c_p, c_p, c_p, c_i64, c_i64, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_p, c_p, c_i32, c_p, c_i32,
+                      c_i32, c_p, c_i64, c_p, c_i32, c_i32, c_p, c_i64, c_p, c_p, c_i64, c_i32, c_p],
     "t2h_rope_freqs": [c_i32, c_i32, c_f64, c_f64, c_p, c_i32],
     "t2h_rope_phases": [c_p, c_i64, c_i32, c_p, c_i32, c_i32, c_p, c_p, c_i32, c_i32, c_p],
     "t2h_activation": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_p],

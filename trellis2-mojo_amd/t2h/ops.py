@@ -256,6 +256,54 @@ def qkv_bias_rmsnorm_rope(qkv, heads: int, head_dim: int, bias=None, gamma_q=Non
     return qkv
 
 
+def attn_pack(q=None, k=None, v=None, mp: int = 0, lp: int = 0, bias_q=None, bias_k=None, bias_v=None, gamma_q=None,
+              gamma_k=None, freqs=None, pos_dim: int = 3, phases=None, coords=None, grid_res: int = 0,
+              use_rope: bool = True, k_transposed: bool = True):
+    """Attention epilogue + head-major packing: q/k/v [rows, H, D] (views of
+    a packed qkv allowed) -> qh [H, mp, D] (scaled by 1/sqrt(D)), k [H, D, lp]
+    (k_transposed) or [H, lp, D], vh [H, lp, D]; pads zero. mp/lp 0 = rows.
+    Returns (qh, k_out, vh), None for an absent input."""
+    ref = next((t for t in (q, k, v) if t is not None), None)
+    if ref is None:
+        raise ValueError("attn_pack: q, k and v are all None")
+    rows, h, d, in_stride = _heads_view(ref, "attn_pack")
+    dt = _dtype(ref, "attn_pack")
+    for t in (q, k, v):
+        if t is not None:
+            if _heads_view(t, "attn_pack") != (rows, h, d, in_stride) or t.dtype != ref.dtype:
+                raise ValueError("attn_pack: q/k/v layouts differ")
+    for g in (gamma_q, gamma_k, bias_q, bias_k, bias_v):
+        if g is not None:
+            _dev(g, "attn_pack")
+            if g.dtype != torch.float32 or g.numel() != h * d or not g.is_contiguous():
+                raise ValueError("attn_pack: gamma/bias must be contiguous float32 [H, D]")
+    mp = mp or rows
+    lp = lp or rows
+    mk = lambda shape: torch.empty(shape, dtype=ref.dtype, device=ref.device)
+    qh = mk((h, mp, d)) if q is not None else None
+    ko = (mk((h, d, lp)) if k_transposed else mk((h, lp, d))) if k is not None else None
+    vh = mk((h, lp, d)) if v is not None else None
+    hold, fp, fd = _host_freqs(freqs if freqs is not None else [])
+    ph_rows = 0
+    if phases is not None:
+        _dev(phases, "attn_pack")
+        if phases.dtype != torch.float32 or not phases.is_contiguous() or phases.shape[-2:] != (d // 2, 2):
+            raise ValueError("apply_rotary_embedding: phases shape mismatch")
+        ph_rows = phases.numel() // d
+    cc = 0
+    if coords is not None:
+        _dev(coords, "attn_pack")
+        if coords.dtype != torch.int32 or not coords.is_contiguous() or coords.shape[0] != rows:
+            raise ValueError("attn_pack: coords must be contiguous int32 [rows, 1+pos_dim]")
+        cc = coords.shape[1]
+    p = lambda t: t.data_ptr() if t is not None else None
+    call("t2h_attn_pack", p(q), p(k), p(v), in_stride, rows, h, d, dt, p(bias_q), p(bias_k), p(bias_v), p(gamma_q),
+         p(gamma_k), int(bool(use_rope)), fp, fd, int(pos_dim), p(phases), ph_rows, p(coords), cc, int(grid_res),
+         p(qh), mp, p(ko), p(vh), lp, int(bool(k_transposed)), _stream())
+    del hold
+    return qh, ko, vh
+
+
 def rope_phases(rows: int, head_dim: int, freqs, pos_dim: int = 3, positions=None, coords=None, grid_res: int = 0,
                 device=None) -> torch.Tensor:
     """Phase table [rows, head_dim/2, 2] (cos, sin) f32."""
