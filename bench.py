@@ -281,10 +281,12 @@ def next_rows(torch, dev, chain, reps):
     qkv = chain.u[:, :3 * C].contiguous()
     q3 = qkv.reshape(T, 3, H, D)
     b3 = chain.bias[:3 * C].reshape(3, H * D)
-    rec("attn_pack_qkv_to_heads", lambda: ops.attn_pack(q3[:, 0], q3[:, 1], q3[:, 2], mp=mp, lp=mp, bias_q=b3[0],
-                                                        bias_k=b3[1], bias_v=b3[2], gamma_q=chain.gq,
-                                                        gamma_k=chain.gk, freqs=chain.freqs, coords=chain.coords),
-        T * 3 * C * e + 3 * mp * C * e + T * 16)
+    for kt in (True, False):   # k as the reference's [H, D, lp], or row-major [H, lp, D]
+        rec(f"attn_pack_k{'t' if kt else 'rows'}",
+            lambda kt=kt: ops.attn_pack(q3[:, 0], q3[:, 1], q3[:, 2], mp=mp, lp=mp, bias_q=b3[0], bias_k=b3[1],
+                                        bias_v=b3[2], gamma_q=chain.gq, gamma_k=chain.gk, freqs=chain.freqs,
+                                        coords=chain.coords, k_transposed=kt),
+            T * 3 * C * e + 3 * mp * C * e + T * 16)
     del qkv, q3
     return res
 

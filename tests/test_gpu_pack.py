@@ -137,6 +137,28 @@ def test_empty_rows_zero_pads(dev):
         assert t.numel() == h * 64 * d and not t.any()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_many_heads_and_table_phases(dev, dtype):
+    """20 heads x 64 (beyond the one-wave-per-row kernel's 16) with a phase
+    table as the position source; mp != lp."""
+    rows, h, d = 999, 20, 64
+    qkv = storage_round(orc.randn(2600, (rows, 3, h, d)), dtype)
+    bias, gq, gk = _params(h, d, 2601)
+    pos = orc.Rng(2602).uniform((rows, 3), 0, 100).astype(np.float32)
+    phases = orc.rope_phases_from_positions(pos, d, orc.rope_freqs(d))
+    mp, lp = pad64(rows), pad64(rows) + 64
+    wq, wk, wv = orc.attn_pack(qkv, h, d, mp, lp, bias.reshape(-1), gq, gk, phases)
+    q, k, v = _views(to_dev(qkv, dev, dtype), h, d)
+    b = to_dev(bias, dev)
+    for kt in (True, False):
+        qh, ko, vh = ops.attn_pack(q, k, v, mp=mp, lp=lp, bias_q=b[0], bias_k=b[1], bias_v=b[2],
+                                   gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(d),
+                                   phases=to_dev(phases, dev), k_transposed=kt)
+        assert_close(qh, wq, dtype, f"qh {dtype}")
+        assert_close(ko if kt else ko.transpose(1, 2), wk, dtype, f"k transposed={kt} {dtype}")
+        assert_close(vh, wv, dtype, f"vh {dtype}")
+
+
 def test_attn_pack_errors(dev):
     h, d = 4, 96
     x = torch.zeros((8, 3, h, d), device=dev)

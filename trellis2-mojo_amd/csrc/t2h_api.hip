@@ -370,6 +370,8 @@ int32_t t2h_attn_pack(const void* q, const void* k, const void* v, int64_t in_st
     if (k_out != nullptr && k_transposed && lp % 8 != 0) return fail(T2H_EINVAL, "%s: transposed k needs lp %% 8 == 0", fn);
     if (qh == nullptr) mp = 0;
     if (k_out == nullptr && vh == nullptr) lp = 0;
+    if (((mp > lp ? mp : lp) + 63) / 64 * heads * 3 >= (int64_t(1) << 24))
+        return fail(T2H_EUNSUPPORTED, "%s: too many rows for one launch", fn);
     if (qh != nullptr && k_out != nullptr && (gamma_q == nullptr) != (gamma_k == nullptr))
         return fail(T2H_EINVAL, "%s: gamma_q and gamma_k must both be given or both NULL", fn);
     RopeSlots tab;

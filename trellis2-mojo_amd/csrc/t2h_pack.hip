@@ -7,16 +7,22 @@
 //   qh [H, mp, D] = q * 1/sqrt(D); k_out [H, D, lp] (transposed) or
 //   [H, lp, D]; vh [H, lp, D]; pad rows rows..mp-1 / rows..lp-1 are zero.
 //
-// A block is 4 waves over a tile of 64 token rows x one head of one tensor.
-// Each 16-lane DPP row of a wave holds one token row's head (lane m: elements
-// [m*E, m*E+E), E = D/16), so a wave instruction covers 4 token rows and the
-// per-head sum of squares is a 4-step DPP row sum; the head's bias and
-// gamma * scale sit in registers for the whole tile. All 16 rows of a wave
-// are loaded (clamped, unconditional) before any math. Row-major outputs are
-// written straight from registers: a wave instruction writes 4 consecutive
-// rows of one head, a contiguous span. The transposed k goes through LDS
-// (64 x (D+1) f32, odd row pitch: conflict-free column reads) and leaves as
-// 16-byte vectors along the token axis.
+// Two kernels:
+// - pack_rows_kernel (row-major outputs: qh, k as [H, lp, D], vh; <= 16
+//   heads): one wave per token row reads the tensor's whole row with
+//   contiguous 16-byte lanes; each 16-lane DPP row holds one head (lane m:
+//   elements [m*E, m*E+E), E = D/16), so the per-head sum of squares is a
+//   4-step DPP row sum and one sincos per lane per row serves every head.
+//   Each head's rows land as contiguous runs of the head-major output.
+// - pack_tile_kernel (the reference's transposed k [H, D, lp], and row-major
+//   outputs beyond 16 heads): a block of 4 waves takes 64 token rows of one
+//   tensor and loops over a group of heads; a wave instruction covers 4 rows
+//   of one head, the rows' cos/sin stay in registers across the heads. The
+//   transposed k goes through LDS (64 x (D+1) f32, odd row pitch:
+//   conflict-free column reads) and leaves as 16-byte vectors along the token
+//   axis.
+// On MI355X the row-major k ([H, lp, D]) is the faster layout: its rows are
+// what an MFMA attention kernel reads as the K operand.
 //
 // Reference: gpu/attention.mojo:507-563 (bias_rms_rope_qkv), 566-594
 // (pack_q_z), 634-662 (pack_kv_z), sequence 987-1013; cross chain q:
@@ -32,8 +38,15 @@ constexpr int kPackRows = 64;
 constexpr int kPackBlock = 256;
 constexpr int kPackIters = kPackRows / 16;   // row groups of 4 per wave
 
-// `order` maps blockIdx.z to the tensor a block packs: 0 = q, 1 = k, 2 = v.
+// The 1-D grid covers row tiles x tensors x head groups, head groups varying
+// fastest. which[] maps the tensor index to the tensor a block packs
+// (0 = q, 1 = k, 2 = v); a block loops over the `hpb` heads of its group, so
+// the RoPE cos/sin of its rows, computed once into registers, serve every
+// head of the group.
 struct PackOrder {
+    int32_t n;        // tensors in this launch
+    int32_t groups;   // head groups = heads / hpb
+    int32_t hpb;      // heads per block
     int8_t which[3];
 };
 
@@ -46,144 +59,306 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
     const int g = lane >> 4;
     const int m = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int which = order.which[blockIdx.z];
-    const int z = blockIdx.y;
-    const int64_t t0 = (int64_t)blockIdx.x * kPackRows;
+    const int64_t b = blockIdx.x;
+    const int hg = (int)(b % order.groups);
+    const int which = order.which[(b / order.groups) % order.n];
+    const int64_t t0 = (b / ((int64_t)order.groups * order.n)) * kPackRows;
     const int64_t extent = which == 0 ? a.mp : a.lp;
     if (t0 >= extent) return;
 
     const T* __restrict__ in = static_cast<const T*>(which == 0 ? a.q : which == 1 ? a.k : a.v);
+    T* __restrict__ out = static_cast<T*>(which == 0 ? a.qh : which == 1 ? a.k_out : a.vh);
     const float* __restrict__ bias = which == 0 ? a.bias_q : which == 1 ? a.bias_k : a.bias_v;
     const float* __restrict__ gamma = which == 0 ? a.gamma_q : which == 1 ? a.gamma_k : nullptr;
     const bool rope = a.use_rope && which < 2;
-    const int col = z * D + m * E;
 
-    float v[kPackIters][E];
-    if (a.rows > 0) {
-#pragma unroll
-        for (int it = 0; it < kPackIters; ++it) {
-            const int64_t t = t0 + it * 16 + wave * 4 + g;
-            const int64_t tl = t < a.rows ? t : a.rows - 1;
-            load_elems<T, E, true>(in + tl * a.in_stride + col, v[it]);
-        }
-    } else {
-#pragma unroll
-        for (int it = 0; it < kPackIters; ++it)
-#pragma unroll
-            for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
-    }
-    float bv[E], gv[E];
-    if (bias != nullptr) load_params<E>(bias + col, bv);
-    if (gamma != nullptr) {
-        load_params<E>(gamma + col, gv);
-#pragma unroll
-        for (int i = 0; i < E; ++i) gv[i] *= a.rms_scale;
-    }
-    int ax[P];
-    float fr[P];
-    if (rope) {
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            ax[j] = tab.axis[m * P + j];
-            fr[j] = tab.freq[m * P + j];
-        }
-    }
-    const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
-
+    // this lane's token rows (clamped for the loads; rows >= a.rows are pads)
+    int64_t rl[kPackIters];
 #pragma unroll
     for (int it = 0; it < kPackIters; ++it) {
         const int64_t t = t0 + it * 16 + wave * 4 + g;
-        const bool valid = t < a.rows;
+        rl[it] = t < a.rows ? t : (a.rows > 0 ? a.rows - 1 : 0);
+    }
+
+    // cos/sin of this lane's P slots for each of its rows, shared by all heads
+    float pc[kPackIters][P], ps[kPackIters][P];
+    if (rope) {
+        if (a.phases != nullptr) {
+#pragma unroll
+            for (int it = 0; it < kPackIters; ++it) {
+                const int64_t l = rl[it] % a.phase_rows;
+                float tmp[2 * P];
+                load_params<2 * P>(a.phases + (l * (D / 2) + m * P) * 2, tmp);
+#pragma unroll
+                for (int j = 0; j < P; ++j) { pc[it][j] = tmp[2 * j]; ps[it][j] = tmp[2 * j + 1]; }
+            }
+        } else {
+            const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
+            int ax[P];
+            float fr[P];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                ax[j] = tab.axis[m * P + j];
+                fr[j] = tab.freq[m * P + j];
+            }
+#pragma unroll
+            for (int it = 0; it < kPackIters; ++it) {
+                float pos[T2H_MAX_POS_DIM];
+                src.get(a.rows > 0 ? rl[it] : 0, pos);
+#pragma unroll
+                for (int j = 0; j < P; ++j) slot_phase(pos, ax[j], fr[j], pc[it][j], ps[it][j]);
+            }
+        }
+    }
+
+    for (int zi = 0; zi < order.hpb; ++zi) {
+        const int z = hg * order.hpb + zi;
+        const int col = z * D + m * E;
+        float v[kPackIters][E];
+        if (a.rows > 0) {
+#pragma unroll
+            for (int it = 0; it < kPackIters; ++it) load_elems<T, E, true>(in + rl[it] * a.in_stride + col, v[it]);
+        } else {
+#pragma unroll
+            for (int it = 0; it < kPackIters; ++it)
+#pragma unroll
+                for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
+        }
+        float bv[E], gv[E];
+        if (bias != nullptr) load_params<E>(bias + col, bv);
+        if (gamma != nullptr) {
+            load_params<E>(gamma + col, gv);
+#pragma unroll
+            for (int i = 0; i < E; ++i) gv[i] *= a.rms_scale;
+        }
+#pragma unroll
+        for (int it = 0; it < kPackIters; ++it) {
+            const int64_t t = t0 + it * 16 + wave * 4 + g;
+            float* x = v[it];
+            if (bias != nullptr) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) x[i] = add_rn(x[i], bv[i]);
+            }
+            if (gamma != nullptr) {
+                const float ss = row16_sum(sum_sq<E>(x));
+                const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+#pragma unroll
+                for (int i = 0; i < E; ++i) x[i] = (x[i] * rn) * gv[i];
+            }
+            if (rope) {
+#pragma unroll
+                for (int j = 0; j < P; ++j) rotate_pair(x[2 * j], x[2 * j + 1], pc[it][j], ps[it][j]);
+            }
+            if (which == 0) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) x[i] = mul_rn(x[i], a.q_scale);
+            }
+            if (t >= a.rows) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) x[i] = 0.0f;
+            }
+            if constexpr (KT) {
+                const int tl = it * 16 + wave * 4 + g;
+#pragma unroll
+                for (int i = 0; i < E; ++i) tile[tl][m * E + i] = round_to<T>(x[i]);
+            } else if (t < extent) {
+                store_elems<T, E, true>(out + ((int64_t)z * extent + t) * D + m * E, x);
+            }
+        }
+        if constexpr (KT) {
+            __syncthreads();
+            constexpr int VE = kPack<T>;            // elements per 16-byte vector
+            constexpr int VPR = kPackRows / VE;     // vectors per output row (one e)
+            for (int vi = threadIdx.x; vi < D * VPR; vi += kPackBlock) {
+                const int e = vi / VPR;
+                const int tq = (vi % VPR) * VE;
+                if (t0 + tq >= extent) continue;
+                float w[VE];
+#pragma unroll
+                for (int i = 0; i < VE; ++i) w[i] = tile[tq + i][e];
+                store_elems<T, VE, true>(out + ((int64_t)z * D + e) * a.lp + t0 + tq, w);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Row-major outputs (qh, k as [H, lp, D], vh) for up to 16 heads: one wave
+// per token row, reading the tensor's whole row (all heads) with contiguous
+// 16-byte lanes, as the QK kernel does. Lane l computes cos/sin of slot l of
+// its row once and ds_bpermute hands each lane the E/2 slots it needs, so the
+// rotation costs one sincos per lane per row for every head. gamma * scale is
+// staged in LDS behind an LDS-only barrier (lgkmcnt(0) + s_barrier) that
+// leaves the row loads in flight. Blocks of the q, k and v of a row tile are
+// adjacent, so the qkv rows are read whole.
+constexpr int kRowWaves = 8;
+constexpr int kRowBlock = kRowWaves * 64;
+
+template <typename T, int D, int NG>
+__global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSlots tab, PackOrder order) {
+    constexpr int E = D / 16;
+    constexpr int P = E / 2;
+    constexpr int HALF = D / 2;
+    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];
+    const int lane = lane_id();
+    const int g = lane >> 4;
+    const int m = lane & 15;
+    const int H = a.heads;
+    const int64_t b = blockIdx.x;
+    const int which = order.which[b % order.n];
+    const int64_t tile = b / order.n;
+    const int64_t extent = which == 0 ? a.mp : a.lp;
+    if (tile * kRowWaves >= extent) return;   // block-uniform
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r = tile * kRowWaves + wave;
+    const bool live = r < a.rows;
+
+    const T* __restrict__ in = static_cast<const T*>(which == 0 ? a.q : which == 1 ? a.k : a.v);
+    T* __restrict__ out = static_cast<T*>(which == 0 ? a.qh : which == 1 ? a.k_out : a.vh);
+    const float* __restrict__ bias = which == 0 ? a.bias_q : which == 1 ? a.bias_k : a.bias_v;
+    const float* __restrict__ gamma = which == 0 ? a.gamma_q : which == 1 ? a.gamma_k : nullptr;
+    const bool rope = a.use_rope && which < 2;
+
+    const int my_slot = lane % HALF;
+    const int my_axis = tab.axis[my_slot];
+    const bool coord_pos = rope && a.phases == nullptr && a.coords != nullptr;
+    float cpos = 0.0f;
+    if (live && coord_pos && my_axis >= 0) cpos = (float)a.coords[r * a.coord_cols + 1 + my_axis];
+
+    const int64_t rl = live ? r : (a.rows > 0 ? a.rows - 1 : 0);
+    float v[NG][E];
+    if (a.rows > 0) {
+#pragma unroll
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+            const int hl = hh < H ? hh : H - 1;
+            load_elems<T, E, true>(in + rl * a.in_stride + (int64_t)hl * D + m * E, v[it]);
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < NG; ++it)
+#pragma unroll
+            for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
+    }
+    if (gamma != nullptr) {
+        for (int i = threadIdx.x; i < H * D; i += kRowBlock) gs[i] = gamma[i] * a.rms_scale;
+    }
+    float pc[P], ps[P];
+    if (rope) {
+        if (a.phases != nullptr) {
+            const int64_t l = rl % a.phase_rows;
+            float tmp[2 * P];
+            load_params<2 * P>(a.phases + (l * HALF + m * P) * 2, tmp);
+#pragma unroll
+            for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
+        } else {
+            float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};
+            if (!coord_pos) {
+                const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
+                src.get(rl, pos);
+            }
+            float c, sn;
+            slot_phase(pos, my_axis, tab.freq[my_slot], c, sn);
+#pragma unroll
+            for (int t = 0; t < P; ++t) {
+                pc[t] = lane_bcast(c, m * P + t);
+                ps[t] = lane_bcast(sn, m * P + t);
+            }
+        }
+    }
+    if (gamma != nullptr) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS stores are done
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    if (r >= extent) return;
+
+#pragma unroll
+    for (int it = 0; it < NG; ++it) {
+        const int hh = 4 * it + g;
+        if (hh >= H) continue;   // uniform over the 16-lane row
         float* x = v[it];
         if (bias != nullptr) {
+            float bv[E];
+            load_params<E>(bias + (int64_t)hh * D + m * E, bv);
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = add_rn(x[i], bv[i]);
         }
         if (gamma != nullptr) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < E; ++i) ss += x[i] * x[i];
-            ss = row16_sum(ss);
+            const float ss = row16_sum(sum_sq<E>(x));
             const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+            const float4* gp = reinterpret_cast<const float4*>(&gs[hh * D + m * E]);
 #pragma unroll
-            for (int i = 0; i < E; ++i) x[i] = (x[i] * rn) * gv[i];
+            for (int c4 = 0; c4 < E / 4; ++c4) {
+                const float4 w = gp[c4];
+                x[4 * c4] = (x[4 * c4] * rn) * w.x;
+                x[4 * c4 + 1] = (x[4 * c4 + 1] * rn) * w.y;
+                x[4 * c4 + 2] = (x[4 * c4 + 2] * rn) * w.z;
+                x[4 * c4 + 3] = (x[4 * c4 + 3] * rn) * w.w;
+            }
         }
         if (rope) {
-            const int64_t tv = valid ? t : 0;
-            float pc[P], ps[P];
-            if (a.phases != nullptr) {
-                const int64_t l = tv % a.phase_rows;
-                float tmp[2 * P];
-                load_params<2 * P>(a.phases + (l * (D / 2) + m * P) * 2, tmp);
 #pragma unroll
-                for (int j = 0; j < P; ++j) { pc[j] = tmp[2 * j]; ps[j] = tmp[2 * j + 1]; }
-            } else {
-                float pos[T2H_MAX_POS_DIM];
-                src.get(tv, pos);
-#pragma unroll
-                for (int j = 0; j < P; ++j) slot_phase(pos, ax[j], fr[j], pc[j], ps[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < P; ++j) {
-                const float re = x[2 * j], im = x[2 * j + 1];
-                x[2 * j] = re * pc[j] - im * ps[j];
-                x[2 * j + 1] = re * ps[j] + im * pc[j];
-            }
+            for (int t = 0; t < P; ++t) rotate_pair(x[2 * t], x[2 * t + 1], pc[t], ps[t]);
         }
         if (which == 0) {
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = mul_rn(x[i], a.q_scale);
         }
-        if (!valid) {
+        if (!live) {
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = 0.0f;
         }
-        if constexpr (KT) {
-            const int tl = it * 16 + wave * 4 + g;
-#pragma unroll
-            for (int i = 0; i < E; ++i) tile[tl][m * E + i] = round_to<T>(x[i]);
-        } else if (t < extent) {
-            T* __restrict__ out = static_cast<T*>(which == 0 ? a.qh : which == 1 ? a.k_out : a.vh);
-            store_elems<T, E, true>(out + ((int64_t)z * extent + t) * D + m * E, x);
-        }
+        store_elems<T, E, true>(out + ((int64_t)hh * extent + r) * D + m * E, x);
     }
+}
 
-    if constexpr (KT) {
-        __syncthreads();
-        constexpr int VE = kPack<T>;            // elements per 16-byte vector
-        constexpr int VPR = kPackRows / VE;     // vectors per output row (one e)
-        T* __restrict__ out = static_cast<T*>(a.k_out);
-        for (int vi = threadIdx.x; vi < D * VPR; vi += kPackBlock) {
-            const int e = vi / VPR;
-            const int tq = (vi % VPR) * VE;
-            if (t0 + tq >= extent) continue;
-            float w[VE];
-#pragma unroll
-            for (int i = 0; i < VE; ++i) w[i] = tile[tq + i][e];
-            store_elems<T, VE, true>(out + ((int64_t)z * D + e) * a.lp + t0 + tq, w);
-        }
+// Heads per block: all of them when the row tiles alone fill the GPU,
+// else the largest divisor of heads that still gives ~8 blocks per CU.
+int heads_per_block(int64_t tiles, int tensors, int heads) {
+    const int64_t want = 8LL * device_cu_count();
+    int best = 1;
+    for (int hpb = 1; hpb <= heads; ++hpb) {
+        if (heads % hpb) continue;
+        if (tiles * tensors * (heads / hpb) >= want || hpb == 1) best = hpb;
     }
+    return best;
 }
 
 template <typename T, int D>
 hipError_t launch_d(const PackArgs& a, const RopeSlots& tab, hipStream_t s) {
     const int64_t ext = a.mp > a.lp ? a.mp : a.lp;
-    const unsigned tiles = (unsigned)((ext + kPackRows - 1) / kPackRows);
+    const int64_t tiles = (ext + kPackRows - 1) / kPackRows;
     PackOrder rows{};
-    int n = 0;
-    if (a.qh != nullptr) rows.which[n++] = 0;
-    if (a.k_out != nullptr && !a.k_transposed) rows.which[n++] = 1;
-    if (a.vh != nullptr) rows.which[n++] = 2;
-    if (n > 0) {
-        hipLaunchKernelGGL((pack_tile_kernel<T, D, false>), dim3(tiles, a.heads, n), dim3(kPackBlock), 0, s, a, tab,
+    if (a.qh != nullptr) rows.which[rows.n++] = 0;
+    if (a.k_out != nullptr && !a.k_transposed) rows.which[rows.n++] = 1;
+    if (a.vh != nullptr) rows.which[rows.n++] = 2;
+    if (rows.n > 0 && a.heads <= 16) {
+        const int64_t blocks = (ext + kRowWaves - 1) / kRowWaves * rows.n;
+        switch ((a.heads + 3) / 4) {
+            case 1: hipLaunchKernelGGL((pack_rows_kernel<T, D, 1>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            case 2: hipLaunchKernelGGL((pack_rows_kernel<T, D, 2>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            case 3: hipLaunchKernelGGL((pack_rows_kernel<T, D, 3>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            default: hipLaunchKernelGGL((pack_rows_kernel<T, D, 4>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+        }
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    } else if (rows.n > 0) {
+        rows.hpb = heads_per_block(tiles, rows.n, a.heads);
+        rows.groups = a.heads / rows.hpb;
+        const int64_t blocks = tiles * rows.groups * rows.n;
+        hipLaunchKernelGGL((pack_tile_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kPackBlock), 0, s, a, tab,
                            rows);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     if (a.k_out != nullptr && a.k_transposed) {
         PackOrder kt{};
+        kt.n = 1;
         kt.which[0] = 1;
-        hipLaunchKernelGGL((pack_tile_kernel<T, D, true>), dim3(tiles, a.heads, 1), dim3(kPackBlock), 0, s, a, tab,
-                           kt);
+        kt.hpb = heads_per_block(tiles, 1, a.heads);
+        kt.groups = a.heads / kt.hpb;
+        hipLaunchKernelGGL((pack_tile_kernel<T, D, true>), dim3((unsigned)(tiles * kt.groups)), dim3(kPackBlock), 0,
+                           s, a, tab, kt);
         return hipGetLastError();
     }
     return hipSuccess;

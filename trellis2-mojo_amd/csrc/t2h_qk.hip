@@ -33,10 +33,6 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 
-__device__ __forceinline__ float lane_bcast(float v, int src_lane) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
-}
-
 constexpr int kTileWaves = 8;
 constexpr int kTileBlock = kTileWaves * 64;
 
@@ -139,10 +135,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
             for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
         }
         if (gamma != nullptr) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < E; ++i) ss += v[it][i] * v[it][i];
-            ss = row16_sum(ss);
+            const float ss = row16_sum(sum_sq<E>(v[it]));
             const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
             float gv[E];
             const float4* gp = reinterpret_cast<const float4*>(&gs[valid ? hh * D + m * E : 0]);
@@ -156,11 +149,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
         }
         if (a.use_rope) {
 #pragma unroll
-            for (int t = 0; t < P; ++t) {
-                const float re = v[it][2 * t], im = v[it][2 * t + 1];
-                v[it][2 * t] = re * pc[t] - im * ps[t];
-                v[it][2 * t + 1] = re * ps[t] + im * pc[t];
-            }
+            for (int t = 0; t < P; ++t) rotate_pair(v[it][2 * t], v[it][2 * t + 1], pc[t], ps[t]);
         }
         if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
     }

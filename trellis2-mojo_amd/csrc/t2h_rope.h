@@ -47,5 +47,30 @@ __device__ __forceinline__ void slot_phase(const float* pos, int ax, float freq,
     }
 }
 
+// One RoPE pair rotation with a fixed rounding sequence (one product and one
+// fused multiply-add per output: re*c - im*s = fma(re, c, -fl(im*s))), so
+// every kernel that rotates a pair produces the same bits whatever the
+// compiler would otherwise contract.
+__device__ __forceinline__ void rotate_pair(float& re, float& im, float c, float s) {
+    const float a = fmaf(re, c, -mul_rn(im, s));
+    const float b = fmaf(re, s, mul_rn(im, c));
+    re = a;
+    im = b;
+}
+
+// Sum of squares of N values in index order, one fused multiply-add each.
+template <int N>
+__device__ __forceinline__ float sum_sq(const float* x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) s = fmaf(x[i], x[i], s);
+    return s;
+}
+
+// v of lane src_lane (ds_bpermute: a lane-indexed read across the wave).
+__device__ __forceinline__ float lane_bcast(float v, int src_lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
+}
+
 }  // namespace
 }  // namespace t2h
