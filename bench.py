@@ -288,6 +288,20 @@ def next_rows(torch, dev, chain, reps):
                                         coords=chain.coords, k_transposed=kt),
             T * 3 * C * e + 3 * mp * C * e + T * 16)
     del qkv, q3
+    # sampler step on the config-5 tokens' 32-channel latent (f32, as the
+    # reference's sampler state), CFG 3.0 + rescale 0.5 over one segment:
+    # statistics pass reads x, v_pos, v_neg; the update pass reads them again
+    # and writes x_prev and pred_x0
+    g = torch.Generator(device=dev).manual_seed(7)
+    lat = [torch.randn((T, 32), generator=g, device=dev) for _ in range(3)]
+    ws = torch.empty(ops.flow_euler_workspace(T, 32, 2), dtype=torch.uint8, device=dev)
+    n = T * 32 * 4
+    rec("flow_euler_step_cfg", lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2],
+                                                           guidance_strength=3.0), 5 * n)
+    rec("flow_euler_step_cfg_rescale", lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2],
+                                                                   guidance_strength=3.0, guidance_rescale=0.5,
+                                                                   seg_offsets=[0, T], workspace=ws), 8 * n)
+    del lat, ws
     return res
 
 

@@ -250,6 +250,36 @@ int32_t t2h_gate_residual_ln_modulate(
     int32_t cols, int32_t dtype, const int64_t* offsets, int32_t nbatch,
     int64_t rows_per_batch, void* stream);
 
+/* ---- flow-matching Euler sampler step ------------------------------------
+ * Replaces the per-step tensor math of FlowEulerSampler._sample_impl
+ * (samplers/flow_euler.mojo:196-210) with _inference's CFG combine and CFG
+ * rescale (151-181, _rescale_pred 75-149) over one flat state of rows x
+ * row_size elements (x_t, v_pos, v_neg, x_prev, pred_x0 all of dtype):
+ *   pred = v_pos                                     (v_neg NULL, or g == 1)
+ *        = v_neg                                     (g == 0)
+ *        = fl(v_pos * f32(g)) + fl(v_neg * f32(1-g))  (otherwise)
+ *   with guidance_rescale > 0 and both predictions, pred is rescaled so that
+ *   each segment's x_0 has the positive branch's std (segments: one per row,
+ *   unbiased std; or the host token offsets seg_offsets_host [n] in rows,
+ *   biased std; rows outside them get pred 0, as in the reference);
+ *   x_prev  = fl(x_t - fl(pred * f32(t - t_prev)))
+ *   pred_x0 = fl(x_t * f32(1 - sigma_min)) - fl(pred * f32(sigma_min + (1 - sigma_min) t))
+ *            (NULL = not written)
+ * The elementwise results are bit-exact with the reference; the rescale's
+ * std is summed in f64 (the reference sums serially in f32). The rescale
+ * needs a device workspace of t2h_flow_euler_workspace() bytes (16-byte
+ * aligned); calls that share a workspace must not overlap. */
+int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size,
+                                 int32_t n_seg_offsets);
+int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos,
+                            const void* v_neg, void* x_prev, void* pred_x0,
+                            int64_t rows, int64_t row_size, int32_t dtype,
+                            double t, double t_prev, double sigma_min,
+                            double guidance_strength, double guidance_rescale,
+                            const int64_t* seg_offsets_host,
+                            int32_t n_seg_offsets, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* ---- resident-block glue over one const buffer ---------------------------
  * The device-resident DiT cross block keeps its per-block glue constants in
  * one f32 buffer `consts` of 12*C floats (gpu/block.mojo:255-289): pairs of

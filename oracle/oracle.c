@@ -7,6 +7,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -452,6 +453,103 @@ void orc_pack_kv(const float* qkv, float* kt, float* vh, int64_t l, int64_t h, i
                 }
             }
         }
+}
+
+/* ------------------------------------------------------------------------ */
+/* FlowEulerSampler: samplers/flow_euler.mojo                                */
+/* ------------------------------------------------------------------------ */
+/* _v_to_xstart (flow_euler.mojo:68-70): _scaled(x_t, 1 - sigma_min) minus
+ * _scaled(v, c), each _scaled one f32 product (_binop_scalar, 56-57). */
+void orc_flow_v_to_xstart(const float* x, const float* v, float* out, int64_t n, double t, double sigma_min) {
+    const float a = (float)(1.0 - sigma_min);
+    const float c = (float)(sigma_min + (1.0 - sigma_min) * t);
+    for (int64_t i = 0; i < n; ++i) {
+        const float xa = x[i] * a;
+        const float vc = v[i] * c;
+        out[i] = xa - vc;
+    }
+}
+
+/* _inference CFG combine (flow_euler.mojo:173-176) */
+void orc_flow_cfg(const float* pos, const float* neg, float* out, int64_t n, double g) {
+    const float gp = (float)g;
+    const float gn = (float)(1.0 - g);
+    for (int64_t i = 0; i < n; ++i) {
+        const float p = pos[i] * gp;
+        const float q = neg[i] * gn;
+        out[i] = p + q;
+    }
+}
+
+/* _rescale_pred (flow_euler.mojo:75-149), serial f32 sums as the reference */
+void orc_flow_rescale(const float* x_t, const float* pred, const float* pred_pos, float* out, int64_t rows,
+                      int64_t row_size, double t, double sigma_min, double guidance_rescale,
+                      const int64_t* seg_offsets, int64_t nseg_offsets) {
+    const int64_t n = rows * row_size;
+    float* x0_pos = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    float* x0_cfg = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    orc_flow_v_to_xstart(x_t, pred_pos, x0_pos, n, t, sigma_min);
+    orc_flow_v_to_xstart(x_t, pred, x0_cfg, n, t, sigma_min);
+    const int varlen = nseg_offsets > 0;
+    const int64_t nb = varlen ? nseg_offsets - 1 : rows;
+    const float gr = (float)guidance_rescale;
+    const float a = (float)(1.0 - sigma_min);
+    const float cc = (float)(sigma_min + (1.0 - sigma_min) * t);
+    for (int64_t i = 0; i < n; ++i) out[i] = 0.0f; /* Tensor[F32](shape) is zero-filled */
+    for (int64_t b = 0; b < nb; ++b) {
+        const int64_t lo = varlen ? seg_offsets[b] * row_size : b * row_size;
+        const int64_t hi = varlen ? seg_offsets[b + 1] * row_size : (b + 1) * row_size;
+        const int64_t m = hi - lo;
+        if (m == 0) continue;
+        float std_pos, std_cfg;
+        if (varlen) { /* VarLenTensor.std: sqrt(mean(x^2) - mean(x)^2), 113-126 */
+            float s1 = 0, s2 = 0, c1 = 0, c2 = 0;
+            for (int64_t e = lo; e < hi; ++e) {
+                s1 += x0_pos[e];
+                s2 += x0_pos[e] * x0_pos[e];
+                c1 += x0_cfg[e];
+                c2 += x0_cfg[e] * x0_cfg[e];
+            }
+            const float mp = s1 / (float)m;
+            const float mc = c1 / (float)m;
+            std_pos = sqrtf(s2 / (float)m - mp * mp);
+            std_cfg = sqrtf(c2 / (float)m - mc * mc);
+        } else { /* unbiased two-pass, 127-143 */
+            float s1 = 0, c1 = 0;
+            for (int64_t e = lo; e < hi; ++e) {
+                s1 += x0_pos[e];
+                c1 += x0_cfg[e];
+            }
+            const float mp = s1 / (float)m;
+            const float mc = c1 / (float)m;
+            float vp = 0, vc = 0;
+            for (int64_t e = lo; e < hi; ++e) {
+                const float dp = x0_pos[e] - mp;
+                const float dc = x0_cfg[e] - mc;
+                vp += dp * dp;
+                vc += dc * dc;
+            }
+            std_pos = sqrtf(vp / (float)(m - 1));
+            std_cfg = sqrtf(vc / (float)(m - 1));
+        }
+        const float ratio = std_pos / std_cfg;
+        for (int64_t e = lo; e < hi; ++e) { /* 144-148 */
+            const float x0r = x0_cfg[e] * ratio;
+            const float x0 = gr * x0r + (1.0f - gr) * x0_cfg[e];
+            out[e] = (a * x_t[e] - x0) / cc;
+        }
+    }
+    free(x0_pos);
+    free(x0_cfg);
+}
+
+/* sample = x_t - (t - t_prev) * v (flow_euler.mojo:210) */
+void orc_flow_step(const float* x, const float* v, float* out, int64_t n, double t, double t_prev) {
+    const float dt = (float)(t - t_prev);
+    for (int64_t i = 0; i < n; ++i) {
+        const float vd = v[i] * dt;
+        out[i] = x[i] - vd;
+    }
 }
 
 /* ------------------------------------------------------------------------ */

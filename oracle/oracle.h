@@ -128,6 +128,20 @@ void orc_pack_q(const float* qkv, float* qh, int64_t l, int64_t h, int64_t d,
 void orc_pack_kv(const float* qkv, float* kt, float* vh, int64_t l, int64_t h,
                  int64_t d, int64_t lp);
 
+/* ---- FlowEulerSampler elementwise math: samplers/flow_euler.mojo:56-149, 151-181, 196-210 */
+/* x0 = fl(x * f32(1 - sigma_min)) - fl(v * f32(sigma_min + (1 - sigma_min) * t)) */
+void orc_flow_v_to_xstart(const float* x, const float* v, float* out, int64_t n, double t, double sigma_min);
+/* pred = fl(pos * f32(g)) + fl(neg * f32(1 - g)) */
+void orc_flow_cfg(const float* pos, const float* neg, float* out, int64_t n, double g);
+/* CFG rescale (_rescale_pred): segments [bounds[b], bounds[b+1]) of the flat
+ * state, bounds = seg_offsets * row_size (varlen, biased std) when
+ * nseg_offsets > 0, else one segment per row of row_size (unbiased std). */
+void orc_flow_rescale(const float* x_t, const float* pred, const float* pred_pos, float* out, int64_t rows,
+                      int64_t row_size, double t, double sigma_min, double guidance_rescale,
+                      const int64_t* seg_offsets, int64_t nseg_offsets);
+/* x_prev = fl(x - fl(v * f32(t - t_prev))) */
+void orc_flow_step(const float* x, const float* v, float* out, int64_t n, double t, double t_prev);
+
 /* ---- TimestepEmbedder.timestep_embedding: sparse_structure_flow.mojo:60-76 */
 void orc_timestep_embedding(const float* t, int64_t n, int64_t dim,
                             double max_period, float* out /* [n, dim] */);

@@ -452,3 +452,85 @@ def attn_pack(qkv, h: int, d: int, mp: int, lp: int, bias=None, gamma_q=None, ga
     qh = pack_q(e, rows, h, d, mp, 3 * h * d)
     kt, vh = pack_kv(e, rows, h, d, lp)
     return qh, kt, vh
+
+
+# ---- FlowEulerSampler (samplers/flow_euler.mojo) --------------------------------
+GUIDANCE_NONE, GUIDANCE_CFG, GUIDANCE_CFG_INTERVAL = 0, 1, 2   # flow_euler.mojo:27-29
+
+
+def flow_v_to_xstart(x, v, t: float, sigma_min: float) -> np.ndarray:
+    x, v = _f32(x), _f32(v)
+    out = np.empty_like(x)
+    lib().orc_flow_v_to_xstart(_p(x), _p(v), _p(out), _i64(x.size), ctypes.c_double(t), ctypes.c_double(sigma_min))
+    return out
+
+
+def flow_cfg(pos, neg, g: float) -> np.ndarray:
+    pos, neg = _f32(pos), _f32(neg)
+    out = np.empty_like(pos)
+    lib().orc_flow_cfg(_p(pos), _p(neg), _p(out), _i64(pos.size), ctypes.c_double(g))
+    return out
+
+
+def flow_rescale(x_t, pred, pred_pos, t: float, sigma_min: float, guidance_rescale: float,
+                 seg_offsets=None) -> np.ndarray:
+    """_rescale_pred on x_t [rows, ...]: one segment per row (dense), or the
+    token segments seg_offsets (varlen)."""
+    x_t, pred, pred_pos = _f32(x_t), _f32(pred), _f32(pred_pos)
+    rows = x_t.shape[0]
+    rs = x_t.size // rows if rows else 0
+    so = np.ascontiguousarray(seg_offsets if seg_offsets is not None else np.zeros(0), dtype=np.int64)
+    out = np.empty_like(x_t)
+    lib().orc_flow_rescale(_p(x_t), _p(pred), _p(pred_pos), _p(out), _i64(rows), _i64(rs), ctypes.c_double(t),
+                           ctypes.c_double(sigma_min), ctypes.c_double(guidance_rescale), _p(so) if so.size else None,
+                           _i64(so.size))
+    return out
+
+
+def flow_step(x, v, t: float, t_prev: float) -> np.ndarray:
+    x, v = _f32(x), _f32(v)
+    out = np.empty_like(x)
+    lib().orc_flow_step(_p(x), _p(v), _p(out), _i64(x.size), ctypes.c_double(t), ctypes.c_double(t_prev))
+    return out
+
+
+def flow_t_seq(steps: int, rescale_t: float):
+    """t_seq of _sample_impl (flow_euler.mojo:195-198), float64."""
+    out = []
+    for i in range(steps + 1):
+        t = 1.0 - float(i) / float(steps)
+        out.append(rescale_t * t / (1.0 + (rescale_t - 1.0) * t))
+    return out
+
+
+def flow_inference(model, x_t, t: float, mode: int, g: float, lo: float, hi: float, gr: float, sigma_min: float,
+                   seg_offsets=None) -> np.ndarray:
+    """_inference (flow_euler.mojo:151-181); model(x_t, t1000, use_neg_cond)."""
+    use_cfg = mode == GUIDANCE_CFG
+    if mode == GUIDANCE_CFG_INTERVAL:
+        use_cfg = lo <= t <= hi
+    if not use_cfg or g == 1.0:
+        return _f32(model(x_t, 1000.0 * t, False))
+    if g == 0.0:
+        return _f32(model(x_t, 1000.0 * t, True))
+    pos = _f32(model(x_t, 1000.0 * t, False))
+    neg = _f32(model(x_t, 1000.0 * t, True))
+    pred = flow_cfg(pos, neg, g)
+    if gr > 0.0:
+        return flow_rescale(x_t, pred, pos, t, sigma_min, gr, seg_offsets)
+    return pred
+
+
+def flow_sample(model, noise, steps: int, rescale_t: float, sigma_min: float, mode: int = GUIDANCE_NONE,
+                g: float = 1.0, lo: float = 0.0, hi: float = 1.0, gr: float = 0.0, seg_offsets=None):
+    """_sample_impl (flow_euler.mojo:183-214). Returns (samples, pred_x_t list, pred_x_0 list)."""
+    sample = _f32(noise).copy()
+    ts = flow_t_seq(steps, rescale_t)
+    xs, x0s = [], []
+    for i in range(steps):
+        t, tp = ts[i], ts[i + 1]
+        v = flow_inference(model, sample, t, mode, g, lo, hi, gr, sigma_min, seg_offsets)
+        x0s.append(flow_v_to_xstart(sample, v, t, sigma_min))
+        sample = flow_step(sample, v, t, tp)
+        xs.append(sample.copy())
+    return sample, xs, x0s

@@ -1,0 +1,157 @@
+"""GPU parity: the flow-matching Euler sampler step (t2h_flow_euler_step) and
+the sampler loop built on it (t2h.sampler.FlowEulerSampler), through the C
+ABI, against the C oracle's restatement of samplers/flow_euler.mojo.
+
+Bars: the CFG combine, the Euler update and pred_x0 are single f32 roundings
+and are compared bit for bit. The CFG rescale's std is summed in f64 on the
+device and serially in f32 by the reference, so the rescaled prediction is
+compared to tolerance; the step divides by cc = f32(sigma_min + (1 -
+sigma_min) t), so the bar is 1e-5 / cc (f32 storage; t >= 0.5 keeps it within
+2e-5). Metric: tests/_parity.py."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from _parity import assert_close, host, max_err, storage_round, to_dev
+from t2h import ops, sampler, workloads
+from t2h._lib import T2HError
+
+pytestmark = pytest.mark.gpu
+SM = 1e-5
+
+
+def _case(seed, shape, dtype=torch.float32):
+    x = storage_round(orc.randn(seed, shape), dtype)
+    pos = storage_round(orc.randn(seed + 1, shape), dtype)
+    neg = storage_round(orc.randn(seed + 2, shape, std=0.5), dtype)
+    return x, pos, neg
+
+
+def _bits(got, want, dtype):
+    w = torch.from_numpy(np.ascontiguousarray(storage_round(want, dtype))).to(dtype)
+    return torch.equal(got.cpu(), w)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_step_no_guidance_and_cfg_bit_exact(dev, dtype):
+    """ss-flow latent shape [2, 8, 16, 16, 16]: Euler step alone and with the
+    CFG combine (g = 3): x_prev and pred_x0 bit-exact."""
+    shape = (2, 8, 16, 16, 16)
+    x, pos, neg = _case(3000, shape, dtype)
+    t, tp = 0.8123, 0.7311
+    xp, x0 = ops.flow_euler_step(to_dev(x, dev, dtype), to_dev(pos, dev, dtype), t, tp, SM)
+    assert _bits(xp, orc.flow_step(x, pos, t, tp), dtype)
+    assert _bits(x0, orc.flow_v_to_xstart(x, pos, t, SM), dtype)
+    xp, x0 = ops.flow_euler_step(to_dev(x, dev, dtype), to_dev(pos, dev, dtype), t, tp, SM,
+                                 v_neg=to_dev(neg, dev, dtype), guidance_strength=3.0)
+    pred = orc.flow_cfg(pos, neg, 3.0)
+    assert _bits(xp, orc.flow_step(x, pred, t, tp), dtype)
+    assert _bits(x0, orc.flow_v_to_xstart(x, pred, t, SM), dtype)
+
+
+def test_step_guidance_strength_edges(dev):
+    """g = 1 uses the positive prediction alone, g = 0 the negative alone,
+    and neither is rescaled (flow_euler.mojo:167-170)."""
+    x, pos, neg = _case(3100, (4, 300))
+    for g, v in ((1.0, pos), (0.0, neg)):
+        xp, _ = ops.flow_euler_step(to_dev(x, dev), to_dev(pos, dev), 0.9, 0.8, SM, v_neg=to_dev(neg, dev),
+                                    guidance_strength=g, guidance_rescale=0.7)
+        assert _bits(xp, orc.flow_step(x, v, 0.9, 0.8), torch.float32)
+
+
+@pytest.mark.parametrize("t", [0.9, 0.55])
+def test_step_rescale_dense(dev, t):
+    """Dense state [2, 8, 16, 16, 16], guidance_rescale 0.7 (the ss stage of
+    pipeline.json): one std per row, unbiased."""
+    shape = (2, 8, 16, 16, 16)
+    x, pos, neg = _case(3200, shape)
+    tp = t - 0.07
+    pred = orc.flow_rescale(x, orc.flow_cfg(pos, neg, 7.5), pos, t, SM, 0.7)
+    xp, x0 = ops.flow_euler_step(to_dev(x, dev), to_dev(pos, dev), t, tp, SM, v_neg=to_dev(neg, dev),
+                                 guidance_strength=7.5, guidance_rescale=0.7)
+    cc = float(np.float32(SM + (1 - SM) * t))
+    assert max_err(x0, orc.flow_v_to_xstart(x, pred, t, SM)) <= 1e-5
+    assert max_err(xp, orc.flow_step(x, pred, t, tp)) <= 1e-5 / cc
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_step_rescale_varlen_config4(dev, dtype):
+    """Varlen state: config-4 token rows (T = 39,804, two batches) x 32
+    latent channels, per-segment biased std (the shape stage, rescale 0.5)."""
+    _, offsets = workloads.config4()
+    shape = (int(offsets[-1]), 32)
+    x, pos, neg = _case(3300, shape, dtype)
+    t, tp = 0.74, 0.66
+    pred = orc.flow_rescale(x, orc.flow_cfg(pos, neg, 5.0), pos, t, SM, 0.5, offsets)
+    xp, x0 = ops.flow_euler_step(to_dev(x, dev, dtype), to_dev(pos, dev, dtype), t, tp, SM,
+                                 v_neg=to_dev(neg, dev, dtype), guidance_strength=5.0, guidance_rescale=0.5,
+                                 seg_offsets=offsets)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    cc = float(np.float32(SM + (1 - SM) * t))
+    assert max_err(xp, storage_round(orc.flow_step(x, pred, t, tp), dtype)) <= tol / cc
+    assert max_err(x0, storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
+
+
+def test_step_rescale_uncovered_rows_and_workspace_reuse(dev):
+    """Rows outside the token segments keep a zero prediction (x_prev = x,
+    pred_x0 = x * a, bit-exact); one workspace serves consecutive calls."""
+    x, pos, neg = _case(3400, (50, 24))
+    segs = np.array([5, 5, 30, 41], np.int64)
+    ws = torch.empty(ops.flow_euler_workspace(50, 24, 4), dtype=torch.uint8, device=dev)
+    for t in (0.95, 0.6):
+        pred = orc.flow_rescale(x, orc.flow_cfg(pos, neg, 3.0), pos, t, SM, 0.7, segs)
+        xp, x0 = ops.flow_euler_step(to_dev(x, dev), to_dev(pos, dev), t, t - 0.1, SM, v_neg=to_dev(neg, dev),
+                                     guidance_strength=3.0, guidance_rescale=0.7, seg_offsets=segs, workspace=ws)
+        want = orc.flow_step(x, pred, t, t - 0.1)
+        assert np.array_equal(host(xp)[:5], x[:5]) and np.array_equal(host(xp)[41:], x[41:])
+        assert np.array_equal(host(x0)[:5], x[:5] * np.float32(1 - SM))
+        assert max_err(xp, want) <= 2e-5
+
+
+def test_sampler_loop_bit_exact_without_rescale(dev):
+    """FlowEulerSampler.sample_cfg_interval with a model whose predictions
+    are exact in f32 on both sides (v = x/2, negative branch -x/4): the whole
+    12-step trajectory matches the oracle's sampler bit for bit, including the
+    guidance interval switching CFG on and off."""
+    noise = orc.randn(3500, (2, 8, 4, 4, 4))
+    dmodel = lambda xt, t1000, neg: xt * (-0.25 if neg else 0.5)
+    omodel = lambda xt, t1000, neg: (xt * np.float32(-0.25 if neg else 0.5)).astype(np.float32)
+    s = sampler.FlowEulerSampler(SM)
+    res = s.sample_cfg_interval(dmodel, to_dev(noise, dev), steps=12, rescale_t=3.0, guidance_strength=3.0,
+                                interval_lo=0.6, interval_hi=0.9)
+    want, xs, x0s = orc.flow_sample(omodel, noise, 12, 3.0, SM, orc.GUIDANCE_CFG_INTERVAL, 3.0, 0.6, 0.9)
+    assert np.array_equal(host(res.samples), want)
+    assert all(np.array_equal(host(a), b) for a, b in zip(res.pred_x_t, xs))
+    assert all(np.array_equal(host(a), b) for a, b in zip(res.pred_x_0, x0s))
+
+
+def test_sampler_loop_with_rescale(dev):
+    """The same loop with guidance_rescale 0.7 on a varlen state: per-step
+    errors of the rescale (f64 vs serial f32 std) stay at the 1e-5 level
+    across 6 steps."""
+    noise = orc.randn(3600, (300, 16))
+    segs = [0, 120, 300]
+    dmodel = lambda xt, t1000, neg: xt * (-0.25 if neg else 0.5)
+    omodel = lambda xt, t1000, neg: (xt * np.float32(-0.25 if neg else 0.5)).astype(np.float32)
+    res = sampler.FlowEulerSampler(SM).sample_cfg(dmodel, to_dev(noise, dev), steps=6, rescale_t=3.0,
+                                                  guidance_strength=3.0, guidance_rescale=0.7, seg_offsets=segs)
+    want, _, _ = orc.flow_sample(omodel, noise, 6, 3.0, SM, orc.GUIDANCE_CFG, 3.0, 0.0, 1.0, 0.7,
+                                 np.array(segs, np.int64))
+    assert max_err(res.samples, want) <= 1e-4
+
+
+def test_step_errors(dev):
+    x = torch.zeros((4, 8), device=dev)
+    with pytest.raises(ValueError, match="workspace"):
+        ops.flow_euler_step(x, x, 0.5, 0.4, SM, v_neg=x, guidance_strength=3.0, guidance_rescale=0.5,
+                            workspace=torch.empty(8, dtype=torch.uint8, device=dev))
+    with pytest.raises(ValueError, match="ordered"):
+        ops.flow_euler_step(x, x, 0.5, 0.4, SM, v_neg=x, guidance_strength=3.0, guidance_rescale=0.5,
+                            seg_offsets=[0, 3, 2])
+    x1 = x.reshape(-1, 1)   # 32 rows
+    with pytest.raises(T2HError, match="more than 64 segments"):
+        ops.flow_euler_step(x1, x1, 0.5, 0.4, SM, v_neg=x1, guidance_strength=3.0, guidance_rescale=0.5,
+                            seg_offsets=list(range(32)) + [32] * 34)
+    with pytest.raises(ValueError, match="size mismatch"):
+        ops.flow_euler_step(x, x[:2], 0.5, 0.4, SM)

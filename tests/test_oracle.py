@@ -378,3 +378,79 @@ def test_packs_are_numpy_transposes():
     # cross-chain stride (q alone, rows h*d apart)
     q = orc.randn(78, (l, h, d))
     assert np.array_equal(orc.pack_q(q.reshape(l, -1), l, h, d, l, h * d)[:, :l], (q * scale).transpose(1, 0, 2))
+
+
+# ---- FlowEulerSampler: samplers/flow_euler.mojo ----------------------------------
+def test_flow_elementwise_exact_f32():
+    """_v_to_xstart, the CFG combine and the Euler update are sequences of
+    single f32 roundings: numpy's IEEE float32 ufuncs give the same bits.
+    Dropping the (1 - sigma_min) factor of c (a plausible slip) changes them."""
+    x, v, w = orc.randn(1600, (5000,)), orc.randn(1601, (5000,)), orc.randn(1602, (5000,))
+    t, tp, sm, g = 0.7371, 0.6012, 1e-5, 3.0
+    a = np.float32(1.0 - sm)
+    c = np.float32(sm + (1.0 - sm) * t)
+    assert np.array_equal(orc.flow_v_to_xstart(x, v, t, sm), x * a - v * c)
+    c_mut = np.float32(sm + t)
+    assert c_mut != c and not np.array_equal(orc.flow_v_to_xstart(x, v, t, sm), x * a - v * c_mut)
+    assert np.array_equal(orc.flow_cfg(v, w, g), v * np.float32(g) + w * np.float32(1.0 - g))
+    assert np.array_equal(orc.flow_step(x, v, t, tp), x - v * np.float32(t - tp))
+
+
+def _rescale_case(seed, rows, rs):
+    x = orc.randn(seed, (rows, rs))
+    pos = orc.randn(seed + 1, (rows, rs))
+    neg = orc.randn(seed + 2, (rows, rs), std=0.5)
+    return x, pos, neg
+
+
+@pytest.mark.parametrize("varlen", [False, True])
+def test_flow_rescale_float64_properties(varlen):
+    """With guidance_rescale 1 the rescaled x_0 of every segment has the
+    positive branch's std (checked in float64 on x_0 = a*x - cc*out); with 0
+    the output is the CFG prediction itself. Segments: one per row (dense)
+    or token offsets (varlen); a dense reading of a varlen state fails the
+    per-segment check."""
+    rows, rs, t, sm = 6, 40, 0.63, 1e-5
+    x, pos, neg = _rescale_case(1700, rows, rs)
+    pred = orc.flow_cfg(pos, neg, 3.0)
+    segs = np.array([0, 2, 6], np.int64) if varlen else None
+    bounds = [(0, 2), (2, 6)] if varlen else [(r, r + 1) for r in range(rows)]
+    a = 1.0 - sm
+    cc = float(np.float32(sm + (1.0 - sm) * t))
+    out = orc.flow_rescale(x, pred, pos, t, sm, 1.0, segs)
+    x0 = a * x.astype(np.float64) - cc * out.astype(np.float64)
+    x0p = a * x.astype(np.float64) - cc * pos.astype(np.float64)
+    for lo, hi in bounds:
+        assert abs(x0[lo:hi].std() / x0p[lo:hi].std() - 1) < 2e-5
+    if varlen:   # the dense (per-row) reading does not satisfy the segment property
+        dense = orc.flow_rescale(x, pred, pos, t, sm, 1.0, None)
+        x0d = a * x.astype(np.float64) - cc * dense.astype(np.float64)
+        assert abs(x0d[2:6].std() / x0p[2:6].std() - 1) > 1e-3
+    out0 = orc.flow_rescale(x, pred, pos, t, sm, 0.0, segs)
+    assert np.max(np.abs(out0 - pred)) < 2e-5 / cc
+
+
+def test_flow_rescale_uncovered_and_empty_segments():
+    """Rows outside the token segments keep a zero prediction; an empty
+    segment is skipped (flow_euler.mojo:100-112)."""
+    x, pos, neg = _rescale_case(1800, 8, 16)
+    pred = orc.flow_cfg(pos, neg, 2.0)
+    out = orc.flow_rescale(x, pred, pos, 0.5, 1e-5, 0.7, np.array([2, 2, 5], np.int64))
+    assert not out[:2].any() and not out[5:].any() and out[2:5].all()
+
+
+def test_flow_schedule_and_sampler_float64():
+    """t_seq = rescale_t*t/(1+(rescale_t-1)*t) over linspace(1, 0) (1.0 and 0.0
+    at the ends; rescale_t 1 is the plain linspace). With v = -x (no
+    guidance) the sampler is explicit Euler for dx/dt = -x backwards in t:
+    x_{i+1} = x_i * (1 + (t_i - t_{i+1})), checked in float64."""
+    ts = orc.flow_t_seq(12, 3.0)
+    assert ts[0] == 1.0 and ts[-1] == 0.0 and all(a > b for a, b in zip(ts, ts[1:]))
+    assert orc.flow_t_seq(4, 1.0) == [1.0, 0.75, 0.5, 0.25, 0.0]
+    x = orc.randn(1900, (3, 7))
+    model = lambda xt, t1000, neg: (-xt).astype(np.float32)
+    out, xs, x0s = orc.flow_sample(model, x, 12, 3.0, 1e-5)
+    want = x.astype(np.float64)
+    for a, b in zip(ts, ts[1:]):
+        want = want * (1.0 + (a - b))
+    assert np.max(np.abs(out - want) / np.abs(want)) < 1e-5 and len(xs) == 12 and len(x0s) == 12

@@ -549,6 +549,96 @@ int32_t t2h_modulation_add(const float* mod, const float* modulation, float* m, 
     return hip_status(launch_modulation_add(mod, modulation, m, n, width, static_cast<hipStream_t>(stream)), fn);
 }
 
+// Flow-matching Euler step: workspace layout = f64 partials [blocks][4], then
+// f32 ratios [nseg] (16-byte aligned).
+static int64_t euler_ws_bytes(int64_t blocks, int64_t nseg) {
+    return blocks * 32 + ((nseg * 4 + 255) / 256) * 256;
+}
+
+int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size, int32_t n_seg_offsets) {
+    if (rows < 0 || row_size < 0 || n_seg_offsets < 0) return -1;
+    const int64_t nseg = n_seg_offsets > 0 ? n_seg_offsets - 1 : rows;
+    const int64_t per_row = (row_size + kEulerChunk - 1) / kEulerChunk;
+    const int64_t blocks = n_seg_offsets > 0 ? (rows * row_size + kEulerChunk - 1) / kEulerChunk + nseg
+                                              : rows * per_row;
+    return euler_ws_bytes(blocks, nseg);
+}
+
+int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev, void* pred_x0,
+                            int64_t rows, int64_t row_size, int32_t dtype, double t, double t_prev,
+                            double sigma_min, double guidance_strength, double guidance_rescale,
+                            const int64_t* seg_offsets_host, int32_t n_seg_offsets, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+    const char* fn = "t2h_flow_euler_step";
+    if (!dtype_ok(dtype)) return fail(T2H_EINVAL, "%s: bad dtype %d", fn, dtype);
+    if (rows < 0 || row_size <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
+    if (n_seg_offsets < 0 || n_seg_offsets == 1) return fail(T2H_EINVAL, "%s: seg_offsets needs >= 2 entries", fn);
+    const int64_t n = rows * row_size;
+    if (n == 0) return ok();
+    if (x_t == nullptr || v_pos == nullptr || x_prev == nullptr) return fail(T2H_EINVAL, "%s: NULL tensor", fn);
+    EulerArgs a{};
+    a.x = x_t;
+    a.v_pos = v_pos;
+    a.v_neg = v_neg;
+    a.x_prev = x_prev;
+    a.pred_x0 = pred_x0;
+    a.n = n;
+    a.row_size = row_size;
+    a.dtype = dtype;
+    // _inference (flow_euler.mojo:167-181): strength 1 -> the positive
+    // prediction alone, 0 -> the negative alone, neither is rescaled
+    a.mode = 0;
+    if (v_neg != nullptr) {
+        if (guidance_strength == 0.0) a.v_pos = v_neg;
+        else if (guidance_strength != 1.0) a.mode = guidance_rescale > 0.0 ? 2 : 1;
+    }
+    a.gp = (float)guidance_strength;
+    a.gn = (float)(1.0 - guidance_strength);
+    a.a = (float)(1.0 - sigma_min);
+    a.cc = (float)(sigma_min + (1.0 - sigma_min) * t);
+    a.dt = (float)(t - t_prev);
+    a.gr = (float)guidance_rescale;
+    a.one_m_gr = 1.0f - a.gr;
+    int64_t blocks = 0, cover_lo = 0, cover_hi = n;
+    if (a.mode == 2) {
+        if (n_seg_offsets > 0) {
+            if (seg_offsets_host == nullptr) return fail(T2H_EINVAL, "%s: NULL seg_offsets", fn);
+            const int nseg = n_seg_offsets - 1;
+            if (nseg > kEulerMaxSeg) return fail(T2H_EUNSUPPORTED, "%s: more than %d segments", fn, kEulerMaxSeg);
+            for (int s = 0; s <= nseg; ++s) {
+                const int64_t o = seg_offsets_host[s];
+                if (o < 0 || o > rows || (s > 0 && o < seg_offsets_host[s - 1]))
+                    return fail(T2H_EINVAL, "%s: seg_offsets must be ordered within [0, rows]", fn);
+                a.bounds[s] = o * row_size;
+            }
+            a.uniform = 0;
+            a.nseg = nseg;
+            for (int s = 0; s < nseg; ++s) {
+                a.blk_base[s] = blocks;
+                blocks += (a.bounds[s + 1] - a.bounds[s] + kEulerChunk - 1) / kEulerChunk;
+            }
+            a.blk_base[nseg] = blocks;
+            cover_lo = a.bounds[0];
+            cover_hi = a.bounds[nseg];
+        } else {
+            a.uniform = 1;
+            if (rows > INT32_MAX) return fail(T2H_EUNSUPPORTED, "%s: too many rows", fn);
+            a.nseg = (int32_t)rows;
+            blocks = rows * ((row_size + kEulerChunk - 1) / kEulerChunk);
+        }
+        const int64_t need = euler_ws_bytes(blocks, a.nseg);
+        if (workspace == nullptr || workspace_bytes < need)
+            return fail(T2H_EINVAL, "%s: rescale needs a %lld-byte workspace", fn, (long long)need);
+        if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(T2H_EINVAL, "%s: workspace alignment", fn);
+        a.partial = static_cast<double*>(workspace);
+        a.ratio = reinterpret_cast<float*>(static_cast<char*>(workspace) + blocks * 32);
+        if (blocks >= (int64_t(1) << 31)) return fail(T2H_EUNSUPPORTED, "%s: state too large", fn);
+    } else if ((n + kEulerChunk - 1) / kEulerChunk >= (int64_t(1) << 31)) {
+        return fail(T2H_EUNSUPPORTED, "%s: state too large", fn);
+    }
+    return hip_status(launch_euler(a, blocks, cover_lo, cover_hi, static_cast<hipStream_t>(stream)), fn);
+}
+
 // Resident-block glue over one const buffer: the pair at `off` is
 // consts[off : off+c], consts[off+c : off+2c] (gpu/block.mojo:255-289).
 static constexpr float kBlockEps = 1e-6f;   // gpu/block.mojo:44

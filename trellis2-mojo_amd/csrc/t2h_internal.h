@@ -102,6 +102,30 @@ struct PackArgs {
     int32_t k_transposed;
 };
 
+// Flow-matching Euler step (t2h_flow_euler_step).
+constexpr int kEulerChunk = 4096;   // elements per block
+constexpr int kEulerMaxSeg = 64;    // varlen segments carried in the kernel arguments
+struct EulerArgs {
+    const void* x;
+    const void* v_pos;
+    const void* v_neg;
+    void* x_prev;
+    void* pred_x0;           // nullptr = not written
+    int64_t n;               // elements
+    int64_t row_size;
+    int32_t dtype;
+    int32_t mode;            // 0: pred = v_pos, 1: CFG combine, 2: CFG + rescale
+    float gp, gn;            // f32(g), f32(1 - g)
+    float a, cc, dt;         // f32(1 - sigma_min), f32(sigma_min + (1 - sigma_min) t), f32(t - t_prev)
+    float gr, one_m_gr;      // f32(guidance_rescale), 1 - that (in f32)
+    int32_t uniform;         // 1: segment = row (dense), 0: bounds[] (varlen)
+    int32_t nseg;
+    int64_t bounds[kEulerMaxSeg + 1];    // element bounds of the varlen segments
+    int64_t blk_base[kEulerMaxSeg + 1];  // first block of each segment
+    double* partial;         // [blocks][4] workspace
+    float* ratio;            // [nseg] workspace
+};
+
 struct PhaseArgs {
     float* out;
     int64_t rows;
@@ -135,6 +159,7 @@ hipError_t launch_ln(const LnArgs& a, hipStream_t s);
 hipError_t launch_qk(const QkArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_phases(const PhaseArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_pack(const PackArgs& a, const RopeSlots& tab, hipStream_t s);
+hipError_t launch_euler(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
 // t2h_eltwise.hip
 hipError_t launch_activation(const EltArgs& a, hipStream_t s);
 hipError_t launch_gate_residual(const EltArgs& a, hipStream_t s);

@@ -45,6 +45,8 @@ _SIGNATURES = {
     "t2h_timestep_embedding": [c_p, c_p, c_i64, c_i32, c_i32, c_f64, c_p],
     "t2h_coords_to_offsets": [c_p, c_i64, c_i32, c_i32, c_p, c_p, c_p],
     "t2h_modulation_add": [c_p, c_p, c_p, c_i64, c_i64, c_p],
+    "t2h_flow_euler_step": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_f64, c_f64, c_f64, c_f64, c_f64, c_p,
+                            c_i32, c_p, c_i64, c_p],
     "t2h_ln_mod_rows": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p],
     "t2h_gate_add_bias_rows": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p],
     "t2h_block_join_ln": [c_p, c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_p],
@@ -56,7 +58,7 @@ _SIGNATURES = {
     "t2h_h_timestep_embedding": [c_p, c_p, c_i64, c_i32, c_f64],
     "t2h_h_coords_to_offsets": [c_p, c_i64, c_i32, c_i32, c_p],
 }
-EXPORTED = ["t2h_version", "t2h_last_error", *_SIGNATURES]
+EXPORTED = ["t2h_version", "t2h_last_error", "t2h_flow_euler_workspace", *_SIGNATURES]
 
 _lib = None
 
@@ -81,6 +83,8 @@ def load(path: str | None = None):
     L.t2h_version.argtypes = []
     L.t2h_last_error.restype = ctypes.c_char_p
     L.t2h_last_error.argtypes = []
+    L.t2h_flow_euler_workspace.restype = c_i64
+    L.t2h_flow_euler_workspace.argtypes = [c_i64, c_i64, c_i32]
     for name, args in _SIGNATURES.items():
         fn = getattr(L, name)
         fn.restype = c_i32

@@ -401,6 +401,43 @@ def modulation_add(mod, modulation) -> torch.Tensor:
     return out
 
 
+# ---- flow-matching Euler sampler step -------------------------------------------
+def flow_euler_workspace(rows: int, row_size: int, n_seg_offsets: int = 0) -> int:
+    return int(_lib.load().t2h_flow_euler_workspace(int(rows), int(row_size), int(n_seg_offsets)))
+
+
+def flow_euler_step(x_t, v_pos, t: float, t_prev: float, sigma_min: float, v_neg=None,
+                    guidance_strength: float = 1.0, guidance_rescale: float = 0.0, seg_offsets=None,
+                    pred_x0: bool = True, workspace=None, x_prev=None):
+    """One Euler step of the flow sampler on x_t [rows, ...]: returns
+    (x_prev, pred_x0 or None). seg_offsets: host token offsets (varlen state)."""
+    _dev(x_t, "flow_euler_step")
+    if not x_t.is_contiguous() or x_t.dim() < 1:
+        raise ValueError("flow_euler_step: x_t must be contiguous")
+    dt = _dtype(x_t, "flow_euler_step")
+    for v in (v_pos, v_neg):
+        if v is not None and (v.shape != x_t.shape or v.dtype != x_t.dtype or not v.is_contiguous()):
+            raise ValueError("Tensor binop: size mismatch")
+    rows = x_t.shape[0]
+    rs = x_t.numel() // rows if rows else 1
+    so = None
+    nso = 0
+    if seg_offsets is not None:
+        so = np.ascontiguousarray(np.asarray(seg_offsets, dtype=np.int64))
+        nso = int(so.size)
+    x_prev = torch.empty_like(x_t) if x_prev is None else x_prev
+    x0 = torch.empty_like(x_t) if pred_x0 else None
+    ws = workspace
+    rescale = v_neg is not None and guidance_strength not in (0.0, 1.0) and guidance_rescale > 0.0
+    if rescale and ws is None:
+        ws = torch.empty(flow_euler_workspace(rows, rs, nso), dtype=torch.uint8, device=x_t.device)
+    p = lambda t: t.data_ptr() if t is not None else None
+    call("t2h_flow_euler_step", x_t.data_ptr(), v_pos.data_ptr(), p(v_neg), x_prev.data_ptr(), p(x0), rows, rs, dt,
+         float(t), float(t_prev), float(sigma_min), float(guidance_strength), float(guidance_rescale),
+         so.ctypes.data if so is not None else None, nso, p(ws), ws.numel() if ws is not None else 0, _stream())
+    return x_prev, x0
+
+
 # ---- resident-block glue over one const buffer ----------------------------------
 def _block_consts(consts, c: int, offs, what: str) -> int:
     _dev(consts, what)
