@@ -167,6 +167,28 @@ def test_fused_join_sparse_and_affine(dev):
     assert_close(yo2, orc.layernorm(xw2, 1e-6, True, w, b), torch.float32, "ungated join + affine LN")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_fused_gated_join_affine_multibatch(dev, dtype):
+    """The block's self join + norm2: per-batch gate with an affine norm over
+    config-4 rows, whose batch boundary (row 19,838) falls inside an 8-row
+    block, so one block mixes batches (the per-batch gate row is read per
+    row; the affine weight/bias are per channel)."""
+    coords, offsets = workloads.config4()
+    assert offsets[1] % 8 != 0
+    t = coords.shape[0]
+    x = storage_round(orc.randn(811, (t, 1536)), dtype)
+    h = storage_round(orc.randn(812, (t, 1536)), dtype)
+    gate = orc.randn(813, (2, 1536), std=0.5)
+    w = orc.randn(814, (1536,), mean=1.0, std=0.1)
+    b = orc.randn(815, (1536,), std=0.1)
+    xo, yo = ops.gate_residual_ln_modulate(to_dev(x, dev, dtype), to_dev(h, dev, dtype), gate=to_dev(gate, dev),
+                                           eps=1e-6, weight=to_dev(w, dev), norm_bias=to_dev(b, dev),
+                                           offsets=to_dev(offsets, dev))
+    xw = storage_round(orc.gate_residual(x, h, gate, offsets=offsets), dtype)
+    assert bits_equal(xo, xw, dtype)
+    assert_close(yo, orc.layernorm(xw, 1e-6, True, w, b), dtype, f"gated join + affine LN {dtype}")
+
+
 def test_modulation_chunk_views(dev):
     """Modulation.chunks (share_mod) -> six strided [B, C] views read in place."""
     b, c = 2, 1536

@@ -3,10 +3,12 @@
 //
 // Fast path: one wave64 per row, the row held in VGPRs (C = 64 * NCH * E with
 // E = 16 B of storage per lane, e.g. C = 1536: f32 NCH 6, f16/bf16 NCH 3), so
-// the two-pass mean/variance never re-reads HBM. The grid has one wave per row
-// (not persistent: many short waves stream HBM better on MI355X), and the
-// per-batch parameter rows are read through L1 at use. Reductions are DPP row
-// sums plus four readlanes. Every output element follows the reference's f32
+// the two-pass mean/variance never re-reads HBM. A block is 8 rows, one wave
+// each, on a non-persistent grid (many short blocks stream HBM better on
+// MI355X than persistent waves). Each wave issues its row loads first; the
+// block then stages the parameter rows of its first row's batch in LDS
+// behind an LDS-only barrier, so the epilogue never waits on L2. Reductions
+// are DPP row sums plus four readlanes. Every output element follows the reference's f32
 // rounding sequence; only the order of the two row sums differs from the
 // reference.
 //
@@ -19,8 +21,12 @@
 namespace t2h {
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-constexpr int kBlock = 64 * kWavesPerBlock;
+#ifndef T2H_LN_WAVES
+#define T2H_LN_WAVES 8
+#endif
+constexpr int kWavesPerBlock = T2H_LN_WAVES;   // fast path: rows per block
+constexpr int kFastBlock = 64 * kWavesPerBlock;
+constexpr int kBlock = 256;                      // generic path
 
 // y = LN epilogue of one centred value d = x - mean (f32), in the reference's
 // order: n = d * inv_std, then n * (1 + scale) + shift (pb holds the already
@@ -32,21 +38,36 @@ __device__ __forceinline__ float ln_epilogue(float d, float inv, int mode, float
     return n;
 }
 
+// E f32 values from LDS (E a multiple of 4, 16-byte aligned).
+template <int E>
+__device__ __forceinline__ void lds_params(const float* p, float* f) {
+    const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int c4 = 0; c4 < E / 4; ++c4) {
+        const float4 w = q[c4];
+        f[4 * c4] = w.x; f[4 * c4 + 1] = w.y; f[4 * c4 + 2] = w.z; f[4 * c4 + 3] = w.w;
+    }
+}
+
 template <typename T, int NCH, bool JOIN>
-__global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
+__global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
     constexpr int E = kPack<T>;
     constexpr int C = 64 * NCH * E;
+    constexpr int NP = JOIN ? 4 : 2;   // staged parameter rows: p0, p1 [, bias, gate]
+    __shared__ __attribute__((aligned(16))) float ps[NP * C];
     const int lane = lane_id();
-    const int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    if (r >= a.rows) return;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r0 = (int64_t)blockIdx.x * kWavesPerBlock;
+    const int64_t r = r0 + wave;
+    const bool live = r < a.rows;
+    const int64_t rl = live ? r : a.rows - 1;   // dead waves load a valid row, store nothing
     const T* __restrict__ x = static_cast<const T*>(a.x);
     const T* __restrict__ h = static_cast<const T*>(a.h);
     T* __restrict__ xo = static_cast<T*>(a.x_out);
     T* __restrict__ yo = static_cast<T*>(a.y_out);
-    const int64_t base = r * (int64_t)C;
-    const bool need_b = a.mode == T2H_LN_MODULATE || (JOIN && a.gate);
-    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    const int64_t base = rl * (int64_t)C;
 
+    // 1. the row loads, all in flight before anything else
     float v[NCH][E];
     float hv[NCH][E];
 #pragma unroll
@@ -54,15 +75,58 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
         load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
         if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
     }
+
+    // 2. stage the parameter rows of the block's first row's batch in LDS
+    //    (modulate: shift and the rounded 1 + scale; affine: weight, bias;
+    //    join: bias and gate rows)
+    const bool need_b = a.mode == T2H_LN_MODULATE || (JOIN && a.gate);
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    const int32_t b0 = need_b ? bm.batch_of(r0) : 0;
+    const int64_t prow = a.mode == T2H_LN_MODULATE ? b0 * a.p_stride : 0;
+    for (int i = threadIdx.x * 4; i < C; i += kFastBlock * 4) {
+        float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+        if (a.mode != T2H_LN_PLAIN) {
+            w0 = *reinterpret_cast<const float4*>(a.p0 + prow + i);
+            w1 = *reinterpret_cast<const float4*>(a.p1 + prow + i);
+            if (a.mode == T2H_LN_MODULATE) {
+                w1.x = add_rn(1.0f, w1.x); w1.y = add_rn(1.0f, w1.y);
+                w1.z = add_rn(1.0f, w1.z); w1.w = add_rn(1.0f, w1.w);
+            }
+        }
+        *reinterpret_cast<float4*>(&ps[i]) = w0;
+        *reinterpret_cast<float4*>(&ps[C + i]) = w1;
+        if (JOIN) {
+            if (a.bias) *reinterpret_cast<float4*>(&ps[2 * C + i]) = *reinterpret_cast<const float4*>(a.bias + i);
+            if (a.gate)
+                *reinterpret_cast<float4*>(&ps[3 * C + i]) =
+                    *reinterpret_cast<const float4*>(a.gate + b0 * a.gate_stride + i);
+        }
+    }
+    // LDS-only barrier: lgkmcnt(0) covers this wave's LDS (and scalar) traffic;
+    // the row loads (vmcnt) stay in flight across it.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (!live) return;
+
+    // rows of another batch than the block's first (only at batch
+    // boundaries) read their per-batch rows (modulate shift/scale, gate) from
+    // global memory; the affine weight/bias and the join bias are per channel
+    // and always come from LDS
     const int32_t b = need_b ? bm.batch_of(r) : 0;
+    const bool staged = b == b0;
 
     if (JOIN) {   // x_out = x + fl(fl(h + bias) * gate[b]), as stored in T
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int col = (c * 64 + lane) * E;
             float jb[E], jg[E];
-            if (a.bias) load_params<E>(a.bias + col, jb);
-            if (a.gate) load_params<E>(a.gate + b * a.gate_stride + col, jg);
+            if (a.bias) lds_params<E>(&ps[2 * C + col], jb);
+            if (a.gate) {
+                if (staged) lds_params<E>(&ps[3 * C + col], jg);
+                else load_params<E>(a.gate + b * a.gate_stride + col, jg);
+            }
 #pragma unroll
             for (int i = 0; i < E; ++i) {
                 float t = a.bias ? add_rn(hv[c][i], jb[i]) : hv[c][i];
@@ -90,21 +154,18 @@ __global__ __launch_bounds__(kBlock) void ln_rows_kernel(LnArgs a) {
     const float var = wave_sum(q) / (float)C;
     const float inv = 1.0f / sqrtf(var + a.eps);
 
-    const int32_t pb_row = (a.mode == T2H_LN_MODULATE) ? b : 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = (c * 64 + lane) * E;
         float pa[E], pb[E];
-        if (a.mode != T2H_LN_PLAIN) {   // per-chunk parameter rows, read through L1 at use
-            load_params<E>(a.p0 + pb_row * a.p_stride + col, pa);
-            load_params<E>(a.p1 + pb_row * a.p_stride + col, pb);
-            if (a.mode == T2H_LN_MODULATE) {
-#pragma unroll
-                for (int i = 0; i < E; ++i) pb[i] = add_rn(1.0f, pb[i]);   // 1 + scale
-            }
+        if (a.mode != T2H_LN_MODULATE || staged) {
+            lds_params<E>(&ps[col], pa);
+            lds_params<E>(&ps[C + col], pb);
         } else {
+            load_params<E>(a.p0 + b * a.p_stride + col, pa);
+            load_params<E>(a.p1 + b * a.p_stride + col, pb);
 #pragma unroll
-            for (int i = 0; i < E; ++i) { pa[i] = 0.0f; pb[i] = 0.0f; }
+            for (int i = 0; i < E; ++i) pb[i] = add_rn(1.0f, pb[i]);   // 1 + scale
         }
         float y[E];
 #pragma unroll
@@ -181,7 +242,7 @@ int resident_blocks(K kernel) {
 template <typename T, int NCH, bool JOIN>
 hipError_t launch_fast(const LnArgs& a, hipStream_t s) {
     const int64_t grid = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
-    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), dim3((unsigned)grid), dim3(kFastBlock), 0, s, a);
     return hipGetLastError();
 }
 
