@@ -151,6 +151,7 @@ struct EltArgs {
     int32_t dtype;
     int32_t kind;          // activation kind / binop op
     BatchArgs batch;
+    int32_t col_tiles;     // row-tiled kernels: blocks across one row (set at launch)
 };
 
 // t2h_norm.hip
