@@ -138,12 +138,17 @@ def time_region(torch, fn, steps):
 
 
 def time_op(torch, fn, reps, flush=None):
-    """Median per-launch ms; with `flush`, the device caches are flushed
-    (>= 1 GiB streamed) before each launch and only the launch is timed."""
+    """Median per-launch ms of one launch between two events. With `flush`,
+    the device caches are flushed (>= 1 GiB streamed) before each launch;
+    without, a short spin kernel runs first. Either way the GPU is still busy
+    when the host enqueues the launch, so the host's call overhead stays
+    outside the timed interval."""
     times = []
     for _ in range(reps):
         if flush is not None:
             flush()
+        else:
+            torch.cuda._sleep(200000)   # ~0.1 ms of GPU spin, no memory traffic
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         fn()

@@ -52,8 +52,9 @@ struct PackOrder {
 
 template <typename T, int D, bool KT>
 __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeSlots tab, PackOrder order) {
-    constexpr int E = D / 16;
-    constexpr int P = E / 2;
+    using L = HeadLanes<T, D>;
+    constexpr int E = L::E;
+    constexpr int P = L::P;
     __shared__ float tile[KT ? kPackRows : 1][KT ? D + 1 : 1];
     const int lane = lane_id();
     const int g = lane >> 4;
@@ -87,10 +88,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
 #pragma unroll
             for (int it = 0; it < kPackIters; ++it) {
                 const int64_t l = rl[it] % a.phase_rows;
-                float tmp[2 * P];
-                load_params<2 * P>(a.phases + (l * (D / 2) + m * P) * 2, tmp);
-#pragma unroll
-                for (int j = 0; j < P; ++j) { pc[it][j] = tmp[2 * j]; ps[it][j] = tmp[2 * j + 1]; }
+                L::phases(a.phases + l * D, m, pc[it], ps[it]);
             }
         } else {
             const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
@@ -98,8 +96,8 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
             float fr[P];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                ax[j] = tab.axis[m * P + j];
-                fr[j] = tab.freq[m * P + j];
+                ax[j] = tab.axis[L::slot(m, j)];
+                fr[j] = tab.freq[L::slot(m, j)];
             }
 #pragma unroll
             for (int it = 0; it < kPackIters; ++it) {
@@ -113,11 +111,10 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
 
     for (int zi = 0; zi < order.hpb; ++zi) {
         const int z = hg * order.hpb + zi;
-        const int col = z * D + m * E;
         float v[kPackIters][E];
         if (a.rows > 0) {
 #pragma unroll
-            for (int it = 0; it < kPackIters; ++it) load_elems<T, E, true>(in + rl[it] * a.in_stride + col, v[it]);
+            for (int it = 0; it < kPackIters; ++it) L::load(in + rl[it] * a.in_stride + (int64_t)z * D, m, v[it]);
         } else {
 #pragma unroll
             for (int it = 0; it < kPackIters; ++it)
@@ -125,9 +122,9 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
                 for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
         }
         float bv[E], gv[E];
-        if (bias != nullptr) load_params<E>(bias + col, bv);
+        if (bias != nullptr) L::params(bias + z * D, m, bv);
         if (gamma != nullptr) {
-            load_params<E>(gamma + col, gv);
+            L::params(gamma + z * D, m, gv);
 #pragma unroll
             for (int i = 0; i < E; ++i) gv[i] *= a.rms_scale;
         }
@@ -160,9 +157,9 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
             if constexpr (KT) {
                 const int tl = it * 16 + wave * 4 + g;
 #pragma unroll
-                for (int i = 0; i < E; ++i) tile[tl][m * E + i] = round_to<T>(x[i]);
+                for (int i = 0; i < E; ++i) tile[tl][L::elem(m, i)] = round_to<T>(x[i]);
             } else if (t < extent) {
-                store_elems<T, E, true>(out + ((int64_t)z * extent + t) * D + m * E, x);
+                L::store(out + ((int64_t)z * extent + t) * D, m, x);
             }
         }
         if constexpr (KT) {
@@ -196,8 +193,10 @@ constexpr int kRowBlock = kRowWaves * 64;
 
 template <typename T, int D, int NG>
 __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSlots tab, PackOrder order) {
-    constexpr int E = D / 16;
-    constexpr int P = E / 2;
+    using L = HeadLanes<T, D>;
+    constexpr int E = L::E;
+    constexpr int P = L::P;
+    constexpr int VE = L::VE;
     constexpr int HALF = D / 2;
     __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];
     const int lane = lane_id();
@@ -232,7 +231,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
         for (int it = 0; it < NG; ++it) {
             const int hh = 4 * it + g;
             const int hl = hh < H ? hh : H - 1;
-            load_elems<T, E, true>(in + rl * a.in_stride + (int64_t)hl * D + m * E, v[it]);
+            L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
         }
     } else {
 #pragma unroll
@@ -247,10 +246,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     if (rope) {
         if (a.phases != nullptr) {
             const int64_t l = rl % a.phase_rows;
-            float tmp[2 * P];
-            load_params<2 * P>(a.phases + (l * HALF + m * P) * 2, tmp);
-#pragma unroll
-            for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
+            L::phases(a.phases + l * HALF * 2, m, pc, ps);
         } else {
             float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};
             if (!coord_pos) {
@@ -261,8 +257,8 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
             slot_phase(pos, my_axis, tab.freq[my_slot], c, sn);
 #pragma unroll
             for (int t = 0; t < P; ++t) {
-                pc[t] = lane_bcast(c, m * P + t);
-                ps[t] = lane_bcast(sn, m * P + t);
+                pc[t] = lane_bcast(c, L::slot(m, t));
+                ps[t] = lane_bcast(sn, L::slot(m, t));
             }
         }
     }
@@ -281,21 +277,25 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
         float* x = v[it];
         if (bias != nullptr) {
             float bv[E];
-            load_params<E>(bias + (int64_t)hh * D + m * E, bv);
+            L::params(bias + (int64_t)hh * D, m, bv);
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = add_rn(x[i], bv[i]);
         }
         if (gamma != nullptr) {
             const float ss = row16_sum(sum_sq<E>(x));
             const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
-            const float4* gp = reinterpret_cast<const float4*>(&gs[hh * D + m * E]);
 #pragma unroll
-            for (int c4 = 0; c4 < E / 4; ++c4) {
-                const float4 w = gp[c4];
-                x[4 * c4] = (x[4 * c4] * rn) * w.x;
-                x[4 * c4 + 1] = (x[4 * c4 + 1] * rn) * w.y;
-                x[4 * c4 + 2] = (x[4 * c4 + 2] * rn) * w.z;
-                x[4 * c4 + 3] = (x[4 * c4 + 3] * rn) * w.w;
+            for (int j = 0; j < L::NC; ++j) {
+                const float4* gp = reinterpret_cast<const float4*>(&gs[hh * D + L::piece(m, j)]);
+#pragma unroll
+                for (int c4 = 0; c4 < VE / 4; ++c4) {
+                    const float4 w = gp[c4];
+                    float* d = &x[j * VE + 4 * c4];
+                    d[0] = (d[0] * rn) * w.x;
+                    d[1] = (d[1] * rn) * w.y;
+                    d[2] = (d[2] * rn) * w.z;
+                    d[3] = (d[3] * rn) * w.w;
+                }
             }
         }
         if (rope) {
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = 0.0f;
         }
-        store_elems<T, E, true>(out + ((int64_t)hh * extent + r) * D + m * E, x);
+        L::store(out + ((int64_t)hh * extent + r) * D, m, x);
     }
 }
 

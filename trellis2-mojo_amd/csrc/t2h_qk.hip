@@ -5,8 +5,10 @@
 // handles kTileWaves consecutive token rows of one tensor (q, k, or the packed
 // qkv's v); blocks for the tensors of a row tile are adjacent, so they share
 // the tile's coords in cache. Each head is one DPP row of 16 lanes (lane m
-// holds elements [m*E, m*E+E), E = head_dim/16), so a wave instruction
-// covers 4 heads and the per-head sum of squares is a 4-step DPP row sum.
+// holds E = head_dim/16 elements: one 16-byte piece at m*E, or for f32 with
+// head_dim 128 two pieces at m*4 and 64 + m*4, so every load instruction is
+// contiguous across the row), so a wave instruction covers 4 heads and the
+// per-head sum of squares is a 4-step DPP row sum.
 // The interleaved RoPE pairs (2p, 2p+1) are lane-local: lane l computes
 // cos/sin of slot l once per row (64 lanes = the 64 slots of head_dim 128)
 // from the row's integer voxel coordinate (or the dense grid index), and
@@ -38,8 +40,10 @@ constexpr int kTileBlock = kTileWaves * 64;
 
 template <typename T, int D, int NG>
 __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots tab) {
-    constexpr int E = D / 16;
-    constexpr int P = E / 2;
+    using L = HeadLanes<T, D>;
+    constexpr int E = L::E;
+    constexpr int P = L::P;
+    constexpr int VE = L::VE;
     constexpr int HALF = D / 2;
     __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];
     const int lane = lane_id();
@@ -60,13 +64,13 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
     if (which == 2) {                      // packed qkv: v += bias_v (block-uniform branch)
         if (!live) return;
         T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
-        for (int e0 = lane * E; e0 < HD; e0 += 64 * E) {
-            float vv[E], bv[E];
-            load_elems<T, E>(vr + e0, vv);
-            load_params<E>(a.bias_v + e0, bv);
+        for (int e0 = lane * VE; e0 < HD; e0 += 64 * VE) {
+            float vv[VE], bv[VE];
+            load_elems<T, VE>(vr + e0, vv);
+            load_params<VE>(a.bias_v + e0, bv);
 #pragma unroll
-            for (int i = 0; i < E; ++i) vv[i] = add_rn(vv[i], bv[i]);
-            store_elems<T, E>(vr + e0, vv);
+            for (int i = 0; i < VE; ++i) vv[i] = add_rn(vv[i], bv[i]);
+            store_elems<T, VE>(vr + e0, vv);
         }
         return;
     }
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
     for (int it = 0; it < NG; ++it) {
         const int hh = 4 * it + g;
         const int hl = hh < H ? hh : H - 1;
-        load_elems<T, E, true>(in + rl * a.in_stride + (int64_t)hl * D + m * E, v[it]);
+        L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
     }
 
     if (gamma != nullptr) {
@@ -99,10 +103,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
     if (a.use_rope) {
         if (a.phases != nullptr) {
             const int64_t l = live ? r % a.phase_rows : 0;
-            float tmp[2 * P];
-            load_params<2 * P>(a.phases + (l * HALF + m * P) * 2, tmp);
-#pragma unroll
-            for (int t = 0; t < P; ++t) { pc[t] = tmp[2 * t]; ps[t] = tmp[2 * t + 1]; }
+            L::phases(a.phases + l * HALF * 2, m, pc, ps);
         } else {
             float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};
             if (!coord_pos) src.get(live ? r : 0, pos);
@@ -110,8 +111,8 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
             slot_phase(pos, my_axis, tab.freq[my_slot], c, s);
 #pragma unroll
             for (int t = 0; t < P; ++t) {
-                pc[t] = lane_bcast(c, m * P + t);
-                ps[t] = lane_bcast(s, m * P + t);
+                pc[t] = lane_bcast(c, L::slot(m, t));
+                ps[t] = lane_bcast(s, L::slot(m, t));
             }
         }
     }
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
         const bool valid = hh < H;
         if (bias != nullptr && valid) {
             float bv[E];
-            load_params<E>(bias + (int64_t)hh * D + m * E, bv);
+            L::params(bias + (int64_t)hh * D, m, bv);
 #pragma unroll
             for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
         }
@@ -138,11 +139,15 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
             const float ss = row16_sum(sum_sq<E>(v[it]));
             const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
             float gv[E];
-            const float4* gp = reinterpret_cast<const float4*>(&gs[valid ? hh * D + m * E : 0]);
 #pragma unroll
-            for (int c4 = 0; c4 < E / 4; ++c4) {
-                const float4 w = gp[c4];
-                gv[4 * c4] = w.x; gv[4 * c4 + 1] = w.y; gv[4 * c4 + 2] = w.z; gv[4 * c4 + 3] = w.w;
+            for (int j = 0; j < L::NC; ++j) {
+                const float4* gp = reinterpret_cast<const float4*>(&gs[(valid ? hh : 0) * D + L::piece(m, j)]);
+#pragma unroll
+                for (int c4 = 0; c4 < VE / 4; ++c4) {
+                    const float4 w = gp[c4];
+                    float* d = &gv[j * VE + 4 * c4];
+                    d[0] = w.x; d[1] = w.y; d[2] = w.z; d[3] = w.w;
+                }
             }
 #pragma unroll
             for (int i = 0; i < E; ++i) v[it][i] = (v[it][i] * rn) * gv[i];
@@ -151,7 +156,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
 #pragma unroll
             for (int t = 0; t < P; ++t) rotate_pair(v[it][2 * t], v[it][2 * t + 1], pc[t], ps[t]);
         }
-        if (valid) store_elems<T, E, true>(out + r * a.out_stride + (int64_t)hh * D + m * E, v[it]);
+        if (valid) L::store(out + r * a.out_stride + (int64_t)hh * D, m, v[it]);
     }
 }
 

@@ -67,6 +67,44 @@ __device__ __forceinline__ float sum_sq(const float* x) {
     return s;
 }
 
+// Lane layout of one head over the 16 lanes of a DPP row: lane m holds
+// E = D/16 elements as NC pieces of VE contiguous elements (16 bytes at
+// most), piece j at element j*16*VE + m*VE, so every load instruction reads
+// one contiguous span across the row (f32 with D = 128: two 16-byte pieces
+// 256 bytes apart). RoPE pairs (2p, 2p+1) stay inside one lane.
+template <typename T, int D>
+struct HeadLanes {
+    static constexpr int E = D / 16;
+    static constexpr int VE = E * (int)sizeof(T) > 16 ? 16 / (int)sizeof(T) : E;
+    static constexpr int NC = E / VE;
+    static constexpr int P = E / 2;
+    __device__ static __forceinline__ int piece(int m, int j) { return j * 16 * VE + m * VE; }
+    // element index of the lane's i-th value, and the slot of its pair t
+    __device__ static __forceinline__ int elem(int m, int i) { return piece(m, i / VE) + i % VE; }
+    __device__ static __forceinline__ int slot(int m, int t) { return elem(m, 2 * t) / 2; }
+    __device__ static __forceinline__ void load(const T* head, int m, float* v) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) load_elems<T, VE, true>(head + piece(m, j), v + j * VE);
+    }
+    __device__ static __forceinline__ void store(T* head, int m, const float* v) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) store_elems<T, VE, true>(head + piece(m, j), v + j * VE);
+    }
+    // f32 parameters of the head (bias, gamma) in the lane's order
+    __device__ static __forceinline__ void params(const float* head, int m, float* f) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) load_params<VE>(head + piece(m, j), f + j * VE);
+    }
+    // the lane's P (cos, sin) pairs of a phase-table row [D/2][2]
+    __device__ static __forceinline__ void phases(const float* row, int m, float* c, float* s) {
+        float tmp[E];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) load_params<VE>(row + piece(m, j), tmp + j * VE);
+#pragma unroll
+        for (int t = 0; t < P; ++t) { c[t] = tmp[2 * t]; s[t] = tmp[2 * t + 1]; }
+    }
+};
+
 // v of lane src_lane (ds_bpermute: a lane-indexed read across the wave).
 __device__ __forceinline__ float lane_bcast(float v, int src_lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
