@@ -1,0 +1,77 @@
+"""GPU parity at sizes past 2^31 elements: every kernel indexes rows and
+elements in 64 bits. Each test fills a device tensor of more than 2^31
+elements, runs the op, and checks sampled rows (first, middle, last, and
+rows straddling the 2^31-element mark) against the C oracle on the same
+rows. Metric and tolerances: tests/_parity.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from _parity import assert_close, bits_equal, host, storage_round
+from t2h import nn, ops
+
+pytestmark = pytest.mark.gpu
+BIG = 1 << 31
+
+
+def _rows(n_rows, cols):
+    """Sample rows: ends, middle, and those around element 2^31."""
+    mark = BIG // cols
+    cand = [0, 1, n_rows // 2, mark - 1, mark, mark + 1, n_rows - 2, n_rows - 1]
+    return np.array(sorted({r for r in cand if 0 <= r < n_rows}), np.int64)
+
+
+def _fill(shape, dtype, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(dtype)
+
+
+def test_gelu_bias_past_2g_elements(dev):
+    rows, cols = (BIG // 6144) + 4099, 6144          # 2.17e9 elements, 4.3 GB f16
+    x = _fill((rows, cols), torch.float16, dev, 1)
+    assert x.numel() > BIG
+    bias = torch.randn(cols, device=dev) * 0.02
+    out = ops.activation(x, ops.ACT_GELU_TANH, bias=bias)
+    idx = _rows(rows, cols)
+    xi = host(x[idx])
+    want = orc.gelu_tanh_bias(xi, host(bias))
+    assert_close(out[idx], want, torch.float16, "GELU rows past 2^31 elements")
+    del x, out
+    torch.cuda.empty_cache()
+
+
+def test_ln_modulate_and_gated_residual_past_2g_elements(dev):
+    rows, cols = (BIG // 1536) + 777, 1536           # 1.4M rows, 4.3 GB f16
+    x = _fill((rows, cols), torch.float16, dev, 2)
+    assert x.numel() > BIG
+    shift, scale = torch.randn(cols, device=dev) * 0.1, torch.randn(cols, device=dev) * 0.1
+    y = ops.ln_modulate(x, 1e-6, shift=shift, scale=scale)
+    idx = _rows(rows, cols)
+    xi = host(x[idx])
+    assert_close(y[idx], orc.ln_modulate(xi, host(shift), host(scale), eps=1e-6), torch.float16, "LN rows")
+    gate = torch.randn(cols, device=dev) * 0.1
+    out = ops.gate_residual(x, y, gate=gate)
+    want = orc.gate_residual(xi, host(y[idx]), host(gate))
+    assert bits_equal(out[idx], storage_round(want, torch.float16), torch.float16)
+    del x, y, out
+    torch.cuda.empty_cache()
+
+
+def test_qk_rmsnorm_rope_past_2g_elements(dev):
+    rows, h, d = (BIG // 1536) + 333, 12, 128
+    q = _fill((rows, h, d), torch.float16, dev, 3)
+    assert q.numel() > BIG
+    coords = torch.zeros((rows, 4), dtype=torch.int32, device=dev)
+    coords[:, 1:] = (torch.arange(rows, device=dev, dtype=torch.int64).unsqueeze(1) //
+                     torch.tensor([16384, 128, 1], device=dev) % 128).to(torch.int32)
+    gq = torch.ones((h, d), device=dev) + torch.randn((h, d), device=dev) * 0.02
+    qo, _ = ops.qk_rmsnorm_rope(q=q, gamma_q=gq, freqs=nn.rope_freqs(d), coords=coords)
+    idx = _rows(rows, h * d)
+    qi, ci = host(q[idx]), coords[idx].cpu().numpy()
+    phases = orc.rope_phases_from_coords(ci, d, orc.rope_freqs(d))
+    want, _ = orc.qk_rms_rope(qi, qi, host(gq), host(gq), phases)
+    assert_close(qo[idx], want, torch.float16, "QK rows past 2^31 elements")
+    del q, qo, coords
+    torch.cuda.empty_cache()
