@@ -75,3 +75,71 @@ def test_qk_rmsnorm_rope_past_2g_elements(dev):
     assert_close(qo[idx], want, torch.float16, "QK rows past 2^31 elements")
     del q, qo, coords
     torch.cuda.empty_cache()
+
+
+# ---- launches past 2^20 blocks take a 2-D grid (block_linear) -----------------
+GRID_X = 1 << 20
+
+
+def test_two_d_grid_ln_and_gelu(dev):
+    """LN with 8 rows per block and GELU with 4 rows per block, both at
+    512 columns, with more than 2^20 blocks."""
+    rows = 8 * GRID_X + 13
+    x = _fill((rows, 512), torch.float16, dev, 11)
+    shift, scale = torch.randn(512, device=dev) * 0.1, torch.randn(512, device=dev) * 0.1
+    y = ops.ln_modulate(x, 1e-6, shift=shift, scale=scale)
+    idx = np.array([0, GRID_X * 8 - 1, GRID_X * 8, rows - 9, rows - 1])
+    assert_close(y[idx], orc.ln_modulate(host(x[idx]), host(shift), host(scale), eps=1e-6), torch.float16,
+                 "LN on a 2-D grid")
+    g = ops.activation(x, ops.ACT_GELU_TANH)
+    idx = np.array([0, 4 * GRID_X - 1, 4 * GRID_X, rows - 1])
+    assert_close(g[idx], orc.activation(host(x[idx]), orc.ACT_GELU_TANH), torch.float16, "GELU on a 2-D grid")
+    del x, y, g
+    torch.cuda.empty_cache()
+
+
+def test_two_d_grid_qk_and_pack(dev):
+    """QK (8 rows per block, q only) and the attention pack (8 rows per block
+    and tensor) past 2^20 blocks, 4 heads x 64."""
+    h, d = 4, 64
+    rows = 8 * GRID_X + 9
+    q = _fill((rows, h, d), torch.float16, dev, 12)
+    coords = torch.zeros((rows, 4), dtype=torch.int32, device=dev)
+    coords[:, 1:] = (torch.arange(rows, device=dev).unsqueeze(1) // torch.tensor([4096, 64, 1], device=dev)
+                     % 64).to(torch.int32)
+    gq = torch.ones((h, d), device=dev)
+    fr = nn.rope_freqs(d)
+    qo, _ = ops.qk_rmsnorm_rope(q=q, gamma_q=gq, freqs=fr, coords=coords)
+    idx = np.array([0, 8 * GRID_X - 1, 8 * GRID_X, rows - 1])
+    ph = orc.rope_phases_from_coords(coords[idx].cpu().numpy(), d, orc.rope_freqs(d))
+    want, _ = orc.qk_rms_rope(host(q[idx]), host(q[idx]), host(gq), host(gq), ph)
+    assert_close(qo[idx], want, torch.float16, "QK on a 2-D grid")
+    del qo
+    # pack: q, k, v views of [n, 3, h, d] with n such that ceil(n / 8) * 3 > 2^20
+    n = (GRID_X // 3 + 1000) * 8 + 5
+    qkv = _fill((n, 3, h, d), torch.float16, dev, 13)
+    mp = (n + 63) // 64 * 64
+    qh, kt, vh = ops.attn_pack(qkv[:, 0], qkv[:, 1], qkv[:, 2], mp=mp, lp=mp, use_rope=False, k_transposed=False)
+    for t in (n - 1, n - 2, 0):
+        src = host(qkv[t])
+        assert np.array_equal(host(vh[:, t]), src[2])
+        assert np.array_equal(host(kt[:, t]), src[1])
+    assert not host(qh[:, n:]).any()
+    del q, coords, qkv, qh, kt, vh
+    torch.cuda.empty_cache()
+
+
+def test_two_d_grid_sampler_rescale(dev):
+    """Dense CFG rescale with one segment per row and more than 2^20 rows:
+    the per-segment ratio pass and the two block passes use 2-D grids."""
+    rows, rs = GRID_X + 7, 4
+    x = _fill((rows, rs), torch.float32, dev, 14)
+    pos = _fill((rows, rs), torch.float32, dev, 15)
+    neg = _fill((rows, rs), torch.float32, dev, 16)
+    xp, _ = ops.flow_euler_step(x, pos, 0.8, 0.7, 1e-5, v_neg=neg, guidance_strength=3.0, guidance_rescale=0.7,
+                                pred_x0=False)
+    idx = np.array([0, GRID_X - 1, GRID_X, rows - 1])
+    xs, ps, ns = host(x[idx]), host(pos[idx]), host(neg[idx])
+    pred = orc.flow_rescale(xs, orc.flow_cfg(ps, ns, 3.0), ps, 0.8, 1e-5, 0.7)
+    want = orc.flow_step(xs, pred, 0.8, 0.7)
+    assert_close(xp[idx], want, torch.float32, "sampler on a 2-D grid")

@@ -370,8 +370,6 @@ int32_t t2h_attn_pack(const void* q, const void* k, const void* v, int64_t in_st
     if (k_out != nullptr && k_transposed && lp % 8 != 0) return fail(T2H_EINVAL, "%s: transposed k needs lp %% 8 == 0", fn);
     if (qh == nullptr) mp = 0;
     if (k_out == nullptr && vh == nullptr) lp = 0;
-    if (((mp > lp ? mp : lp) + 63) / 64 * heads * 3 >= (int64_t(1) << 24))
-        return fail(T2H_EUNSUPPORTED, "%s: too many rows for one launch", fn);
     if (qh != nullptr && k_out != nullptr && (gamma_q == nullptr) != (gamma_k == nullptr))
         return fail(T2H_EINVAL, "%s: gamma_q and gamma_k must both be given or both NULL", fn);
     RopeSlots tab;
@@ -632,9 +630,9 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_ne
         if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(T2H_EINVAL, "%s: workspace alignment", fn);
         a.partial = static_cast<double*>(workspace);
         a.ratio = reinterpret_cast<float*>(static_cast<char*>(workspace) + blocks * 32);
-        if (blocks >= (int64_t(1) << 31)) return fail(T2H_EUNSUPPORTED, "%s: state too large", fn);
-    } else if ((n + kEulerChunk - 1) / kEulerChunk >= (int64_t(1) << 31)) {
-        return fail(T2H_EUNSUPPORTED, "%s: state too large", fn);
+        a.nblocks = blocks;
+    } else {
+        a.nblocks = (n + kEulerChunk - 1) / kEulerChunk;
     }
     return hip_status(launch_euler(a, blocks, cover_lo, cover_hi, static_cast<hipStream_t>(stream)), fn);
 }

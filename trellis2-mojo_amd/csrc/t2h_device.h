@@ -243,4 +243,8 @@ struct BatchMap {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
+// Linear block index of a launch on grid_1d()'s grid (a second grid
+// dimension only past 2^20 blocks; see t2h_internal.h).
+__device__ __forceinline__ int64_t block_linear() { return (int64_t)blockIdx.y * gridDim.x + blockIdx.x; }
+
 }  // namespace t2h

@@ -94,17 +94,18 @@ struct Tile {
 // from the host: no 64-bit division per wave, none at all for row-wide blocks.
 template <int V>
 __device__ __forceinline__ bool tile_of(const EltArgs& a, Tile& t) {
-    const uint32_t b = blockIdx.x;
-    uint32_t rt, cb;
+    const int64_t b = block_linear();
+    int64_t rt, cb;
     if (a.col_tiles == 1) {
         rt = b;
         cb = 0;
     } else {
-        rt = b / (uint32_t)a.col_tiles;
-        cb = b - rt * (uint32_t)a.col_tiles;
+        rt = b / a.col_tiles;
+        cb = b - rt * a.col_tiles;
     }
-    t.col0 = ((int64_t)cb * blockDim.x + threadIdx.x) * V;
-    t.r0 = (int64_t)rt * kRpt;
+    t.col0 = (cb * blockDim.x + threadIdx.x) * V;
+    t.r0 = rt * kRpt;
+    if (t.r0 >= a.rows) return false;   // past the last row tile of a 2-D grid
     const int64_t left = a.rows - t.r0;
     t.nrows = left < kRpt ? (int)left : kRpt;
     return t.col0 < a.cols;
@@ -346,7 +347,7 @@ hipError_t tile_launch(K kernel, EltArgs a, hipStream_t s) {
     const int64_t rt = (a.rows + kRpt - 1) / kRpt;
     const int64_t ct = (a.cols + bw - 1) / bw;
     a.col_tiles = (int32_t)ct;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)(rt * ct)), dim3(tile_block<V>(a)), 0, s, a);
+    hipLaunchKernelGGL(kernel, grid_1d(rt * ct), dim3(tile_block<V>(a)), 0, s, a);
     return hipGetLastError();
 }
 

@@ -122,6 +122,7 @@ struct EulerArgs {
     int32_t nseg;
     int64_t bounds[kEulerMaxSeg + 1];    // element bounds of the varlen segments
     int64_t blk_base[kEulerMaxSeg + 1];  // first block of each segment
+    int64_t nblocks;         // blocks of the statistics / elementwise passes
     double* partial;         // [blocks][4] workspace
     float* ratio;            // [nseg] workspace
 };
@@ -153,6 +154,16 @@ struct EltArgs {
     BatchArgs batch;
     int32_t col_tiles;     // row-tiled kernels: blocks across one row (set at launch)
 };
+
+// Grid of nblocks blocks. A dispatch counts work-items in 32 bits per grid
+// dimension, so past 2^20 blocks the grid becomes 2^20 x ceil(nblocks/2^20);
+// kernels launched on it index blocks with block_linear() and return when it
+// is past their last block.
+constexpr int64_t kGridX = int64_t(1) << 20;
+inline dim3 grid_1d(int64_t nblocks) {
+    if (nblocks <= kGridX) return dim3((unsigned)nblocks);
+    return dim3((unsigned)kGridX, (unsigned)((nblocks + kGridX - 1) / kGridX));
+}
 
 // t2h_norm.hip
 hipError_t launch_ln(const LnArgs& a, hipStream_t s);

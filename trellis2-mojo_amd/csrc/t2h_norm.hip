@@ -57,7 +57,8 @@ __global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
     __shared__ __attribute__((aligned(16))) float ps[NP * C];
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t r0 = (int64_t)blockIdx.x * kWavesPerBlock;
+    const int64_t r0 = block_linear() * kWavesPerBlock;
+    if (r0 >= a.rows) return;   // past the last row of a 2-D grid (block-uniform)
     const int64_t r = r0 + wave;
     const bool live = r < a.rows;
     const int64_t rl = live ? r : a.rows - 1;   // dead waves load a valid row, store nothing
@@ -242,7 +243,7 @@ int resident_blocks(K kernel) {
 template <typename T, int NCH, bool JOIN>
 hipError_t launch_fast(const LnArgs& a, hipStream_t s) {
     const int64_t grid = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
-    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), dim3((unsigned)grid), dim3(kFastBlock), 0, s, a);
+    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), grid_1d(grid), dim3(kFastBlock), 0, s, a);
     return hipGetLastError();
 }
 

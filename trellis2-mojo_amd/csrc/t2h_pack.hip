@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
     const int g = lane >> 4;
     const int m = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t b = blockIdx.x;
+    const int64_t b = block_linear();
     const int hg = (int)(b % order.groups);
     const int which = order.which[(b / order.groups) % order.n];
     const int64_t t0 = (b / ((int64_t)order.groups * order.n)) * kPackRows;
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     const int g = lane >> 4;
     const int m = lane & 15;
     const int H = a.heads;
-    const int64_t b = blockIdx.x;
+    const int64_t b = block_linear();
     const int which = order.which[b % order.n];
     const int64_t tile = b / order.n;
     const int64_t extent = which == 0 ? a.mp : a.lp;
@@ -337,17 +337,17 @@ hipError_t launch_d(const PackArgs& a, const RopeSlots& tab, hipStream_t s) {
     if (rows.n > 0 && a.heads <= 16) {
         const int64_t blocks = (ext + kRowWaves - 1) / kRowWaves * rows.n;
         switch ((a.heads + 3) / 4) {
-            case 1: hipLaunchKernelGGL((pack_rows_kernel<T, D, 1>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
-            case 2: hipLaunchKernelGGL((pack_rows_kernel<T, D, 2>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
-            case 3: hipLaunchKernelGGL((pack_rows_kernel<T, D, 3>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
-            default: hipLaunchKernelGGL((pack_rows_kernel<T, D, 4>), dim3((unsigned)blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            case 1: hipLaunchKernelGGL((pack_rows_kernel<T, D, 1>), grid_1d(blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            case 2: hipLaunchKernelGGL((pack_rows_kernel<T, D, 2>), grid_1d(blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            case 3: hipLaunchKernelGGL((pack_rows_kernel<T, D, 3>), grid_1d(blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
+            default: hipLaunchKernelGGL((pack_rows_kernel<T, D, 4>), grid_1d(blocks), dim3(kRowBlock), 0, s, a, tab, rows); break;
         }
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     } else if (rows.n > 0) {
         rows.hpb = heads_per_block(tiles, rows.n, a.heads);
         rows.groups = a.heads / rows.hpb;
         const int64_t blocks = tiles * rows.groups * rows.n;
-        hipLaunchKernelGGL((pack_tile_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kPackBlock), 0, s, a, tab,
+        hipLaunchKernelGGL((pack_tile_kernel<T, D, false>), grid_1d(blocks), dim3(kPackBlock), 0, s, a, tab,
                            rows);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
@@ -357,7 +357,7 @@ hipError_t launch_d(const PackArgs& a, const RopeSlots& tab, hipStream_t s) {
         kt.which[0] = 1;
         kt.hpb = heads_per_block(tiles, 1, a.heads);
         kt.groups = a.heads / kt.hpb;
-        hipLaunchKernelGGL((pack_tile_kernel<T, D, true>), dim3((unsigned)(tiles * kt.groups)), dim3(kPackBlock), 0,
+        hipLaunchKernelGGL((pack_tile_kernel<T, D, true>), grid_1d(tiles * kt.groups), dim3(kPackBlock), 0,
                            s, a, tab, kt);
         return hipGetLastError();
     }

@@ -54,10 +54,12 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
     const int has_q = a.q_in != nullptr, has_k = a.k_in != nullptr;
     const int has_v = a.v != nullptr && a.bias_v != nullptr;
     const int upr = has_q + has_k + has_v;
-    int which = (int)(blockIdx.x % upr);   // 0 = q, 1 = k, 2 = v (absent tensors skipped)
+    const int64_t b = block_linear();
+    int which = (int)(b % upr);   // 0 = q, 1 = k, 2 = v (absent tensors skipped)
     if (!has_q) ++which;
     if (which == 1 && !has_k) ++which;
-    const int64_t tile = blockIdx.x / upr;
+    const int64_t tile = b / upr;
+    if (tile * kTileWaves >= a.rows) return;   // past the last tile of a 2-D grid (block-uniform)
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t r = tile * kTileWaves + wave;
     const bool live = r < a.rows;
@@ -264,7 +266,7 @@ template <typename T, int D, int NG>
 hipError_t launch_fast(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
     const int upr = (a.q_in != nullptr) + (a.k_in != nullptr) + (a.v != nullptr && a.bias_v != nullptr);
     const int64_t tiles = (a.rows + kTileWaves - 1) / kTileWaves;
-    hipLaunchKernelGGL((qk_tile_kernel<T, D, NG>), dim3((unsigned)(tiles * upr)), dim3(kTileBlock), 0, s, a, tab);
+    hipLaunchKernelGGL((qk_tile_kernel<T, D, NG>), grid_1d(tiles * upr), dim3(kTileBlock), 0, s, a, tab);
     return hipGetLastError();
 }
 

@@ -78,9 +78,11 @@ __device__ __forceinline__ void block_sum4(double (&v)[4], double (*sh)[4]) {
 template <typename T>
 __global__ __launch_bounds__(kEulerBlock) void euler_stats_kernel(EulerArgs a) {
     __shared__ double sh[kEulerBlock][4];
+    const int64_t b = block_linear();
+    if (b >= a.nblocks) return;
     int s;
     int64_t lo, hi;
-    SegMap::locate(a, blockIdx.x, s, lo, hi);
+    SegMap::locate(a, b, s, lo, hi);
     const T* __restrict__ x = static_cast<const T*>(a.x);
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
     for (int64_t e = lo + threadIdx.x; e < hi; e += kEulerBlock) {
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(kEulerBlock) void euler_stats_kernel(EulerArgs a) {
     }
     block_sum4(acc, sh);
     if (threadIdx.x == 0) {
-        double* p = a.partial + (int64_t)blockIdx.x * 4;
+        double* p = a.partial + b * 4;
 #pragma unroll
         for (int k = 0; k < 4; ++k) p[k] = acc[k];
     }
@@ -105,7 +107,9 @@ __global__ __launch_bounds__(kEulerBlock) void euler_stats_kernel(EulerArgs a) {
 // One block per segment: fixed-order sum of the segment's block partials.
 __global__ __launch_bounds__(kEulerBlock) void euler_ratio_kernel(EulerArgs a) {
     __shared__ double sh[kEulerBlock][4];
-    const int s = blockIdx.x;
+    const int64_t sl = block_linear();
+    if (sl >= a.nseg) return;
+    const int s = (int)sl;
     int64_t b0, b1, m;
     if (a.uniform) {
         const int64_t nb = (a.row_size + kEulerChunk - 1) / kEulerChunk;
@@ -143,12 +147,14 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
     const T* __restrict__ x = static_cast<const T*>(a.x);
     T* __restrict__ xp = static_cast<T*>(a.x_prev);
     T* __restrict__ x0o = static_cast<T*>(a.pred_x0);
+    const int64_t b = block_linear();
+    if (b >= a.nblocks) return;
     int s = 0;
     int64_t lo, hi;
     if (a.mode == 2) {
-        SegMap::locate(a, blockIdx.x, s, lo, hi);
+        SegMap::locate(a, b, s, lo, hi);
     } else {
-        lo = (int64_t)blockIdx.x * kEulerChunk;
+        lo = b * kEulerChunk;
         hi = min(lo + kEulerChunk, a.n);
     }
     const float ratio = a.mode == 2 ? a.ratio[s] : 0.0f;
@@ -186,9 +192,9 @@ template <typename T>
 hipError_t launch_typed(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t st) {
     if (a.mode == 2) {
         if (blocks > 0) {
-            hipLaunchKernelGGL(euler_stats_kernel<T>, dim3((unsigned)blocks), dim3(kEulerBlock), 0, st, a);
-            hipLaunchKernelGGL(euler_ratio_kernel, dim3((unsigned)a.nseg), dim3(kEulerBlock), 0, st, a);
-            hipLaunchKernelGGL(euler_apply_kernel<T>, dim3((unsigned)blocks), dim3(kEulerBlock), 0, st, a);
+            hipLaunchKernelGGL(euler_stats_kernel<T>, grid_1d(blocks), dim3(kEulerBlock), 0, st, a);
+            hipLaunchKernelGGL(euler_ratio_kernel, grid_1d(a.nseg), dim3(kEulerBlock), 0, st, a);
+            hipLaunchKernelGGL(euler_apply_kernel<T>, grid_1d(blocks), dim3(kEulerBlock), 0, st, a);
         }
         if (cover_lo > 0) {
             const int64_t g = (cover_lo + kEulerBlock - 1) / kEulerBlock;
@@ -201,8 +207,7 @@ hipError_t launch_typed(const EulerArgs& a, int64_t blocks, int64_t cover_lo, in
                                0, st, a, cover_hi, a.n);
         }
     } else {
-        hipLaunchKernelGGL(euler_apply_kernel<T>, dim3((unsigned)((a.n + kEulerChunk - 1) / kEulerChunk)),
-                           dim3(kEulerBlock), 0, st, a);
+        hipLaunchKernelGGL(euler_apply_kernel<T>, grid_1d(a.nblocks), dim3(kEulerBlock), 0, st, a);
     }
     return hipGetLastError();
 }
