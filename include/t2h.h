@@ -76,6 +76,8 @@ extern "C" {
 #define T2H_OP_SUB 1
 #define T2H_OP_MUL 2
 #define T2H_OP_DIV 3
+#define T2H_OP_RSUB 4   /* other - x: _binop_scalar(reverse=True), sparse/tensor.mojo:200-203 */
+#define T2H_OP_RDIV 5   /* other / x */
 
 /* limits */
 #define T2H_MAX_HALF_HEAD 128      /* head_dim <= 256 */
@@ -112,7 +114,9 @@ int32_t t2h_modulate(const void* x, void* out, int64_t rows, int32_t cols,
 
 /* SparseTensor.elemwise_batch (sparse/basic.mojo:433-436 ->
  * Tensor._binop_rows sparse/tensor.mojo:205-219): out[r,:] = x[r,:] OP
- * other[b(r), :]; other_cols == cols or 1 (a per-batch scalar). Bit-exact. */
+ * other[b(r), :]; other_cols == cols or 1 (a per-batch scalar). With one
+ * batch and other_cols 1 this is Tensor._binop_scalar (sparse/tensor.mojo:
+ * 200-203); T2H_OP_RSUB / T2H_OP_RDIV are its reverse forms. Bit-exact. */
 int32_t t2h_binop_rows(const void* x, const float* other, void* out,
                        int64_t rows, int32_t cols, int32_t other_cols,
                        int32_t dtype, int32_t op, const int64_t* offsets,

@@ -114,3 +114,38 @@ def test_host_wrapper_errors(dev):
                              1, 0)
     assert rc == 0
     assert np.max(np.abs(out - orc.layernorm(x, 1e-6))) < 1e-5
+
+
+def test_varlen_elemwise_reference_cases(dev):
+    """tests/parity/test_sparse_basic.mojo:73-91 on the device: scalar ops,
+    flat add, negation, per-batch [B, 1] and [B, C] broadcasts; plus the
+    reverse scalar forms (value - x, value / x)."""
+    feats = torch.arange(1, 11, dtype=torch.float32, device=dev).reshape(5, 2)
+    x = sparse.VarLenTensor(feats, [0, 2, 5])
+    y = (x + 1.0) * 2.0
+    assert y.feats.reshape(-1)[0].item() == 4.0 and y.feats.reshape(-1)[9].item() == 22.0
+    z = x + x
+    assert z.feats.reshape(-1)[3].item() == 8.0
+    n = -x
+    assert n.feats.reshape(-1)[0].item() == -1.0
+    b = torch.tensor([[10.0], [100.0]], device=dev)
+    w = x.elemwise_batch(b, sparse.OP_ADD)
+    assert w.feats.reshape(-1)[0].item() == 11.0 and w.feats.reshape(-1)[4].item() == 105.0
+    b2 = torch.tensor([[10.0, 20.0], [100.0, 200.0]], device=dev)
+    w2 = x.elemwise_batch(b2, sparse.OP_ADD)
+    assert w2.feats.reshape(-1)[1].item() == 22.0 and w2.feats.reshape(-1)[9].item() == 210.0
+    f = host(feats)
+    assert np.array_equal(host(x.elemwise_scalar(1.0, sparse.OP_SUB, reverse=True).feats), np.float32(1.0) - f)
+    assert np.array_equal(host(x.elemwise_scalar(3.0, sparse.OP_DIV, reverse=True).feats), np.float32(3.0) / f)
+    assert np.array_equal(host((x / 3.0).feats), f / np.float32(3.0))
+    assert np.array_equal(host((x - 0.5).feats), f - np.float32(0.5))
+    with pytest.raises(ValueError, match="batch size mismatch"):
+        x.elemwise_batch(torch.ones((3, 1), device=dev), sparse.OP_ADD)
+
+
+def test_sparse_vl_view(dev):
+    coords, offsets = workloads.config4()
+    st = sparse.SparseTensor(torch.zeros((coords.shape[0], 4), device=dev), to_dev(coords, dev), 2)
+    v = st.vl
+    assert v.offsets == [int(o) for o in offsets] and v.feats is st.feats
+    assert v.batch_size() == 2

@@ -243,7 +243,7 @@ int32_t t2h_binop_rows(const void* x, const float* other, void* out, int64_t row
     if (!dtype_ok(dtype)) return fail(T2H_EINVAL, "%s: bad dtype %d", fn, dtype);
     if (rows < 0 || cols <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
     if (other_cols != cols && other_cols != 1) return fail(T2H_EINVAL, "Tensor._binop_rows: incompatible row size");
-    if (op < T2H_OP_ADD || op > T2H_OP_DIV) return fail(T2H_EINVAL, "%s: bad op %d", fn, op);
+    if (op < T2H_OP_ADD || op > T2H_OP_RDIV) return fail(T2H_EINVAL, "%s: bad op %d", fn, op);
     if (int32_t rc = check_batch(offsets, nbatch, rows_per_batch, fn)) return rc;
     if (rows == 0) return ok();
     if (x == nullptr || out == nullptr || other == nullptr) return fail(T2H_EINVAL, "%s: NULL tensor", fn);

@@ -216,7 +216,9 @@ __device__ __forceinline__ float apply_op(float x, float y, int op) {
         case T2H_OP_ADD: return add_rn(x, y);
         case T2H_OP_SUB: return sub_rn(x, y);
         case T2H_OP_MUL: return mul_rn(x, y);
-        default: return __fdiv_rn(x, y);
+        case T2H_OP_DIV: return __fdiv_rn(x, y);
+        case T2H_OP_RSUB: return sub_rn(y, x);
+        default: return __fdiv_rn(y, x);
     }
 }
 

@@ -19,7 +19,7 @@ from ._lib import BF16, F16, F32, LN_AFFINE, LN_MODULATE, LN_PLAIN, call
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 ACT_RELU, ACT_SILU, ACT_GELU, ACT_GELU_TANH = 0, 1, 2, 3
-OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
+OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_RSUB, OP_RDIV = 0, 1, 2, 3, 4, 5
 
 
 def _stream() -> int:

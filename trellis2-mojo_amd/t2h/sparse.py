@@ -20,6 +20,116 @@ from . import ops
 from .nn import rope_freqs
 
 OP_ADD, OP_SUB, OP_MUL, OP_DIV = ops.OP_ADD, ops.OP_SUB, ops.OP_MUL, ops.OP_DIV
+_REVERSE = {OP_SUB: ops.OP_RSUB, OP_DIV: ops.OP_RDIV, OP_ADD: OP_ADD, OP_MUL: OP_MUL}
+
+
+def _offsets_ok(offsets, total_rows: int) -> bool:
+    """sparse/basic.mojo:76-82."""
+    if len(offsets) < 1 or offsets[0] != 0:
+        return False
+    if any(b < a for a, b in zip(offsets, offsets[1:])):
+        return False
+    return offsets[-1] == total_rows
+
+
+class VarLenTensor:
+    """feats [T, *tail] with host offsets [B+1]: batch b owns rows
+    [offsets[b], offsets[b+1]) (sparse/basic.mojo:89-247). The tensor math
+    runs in libt2h kernels (bit-exact f32 sequences); the offsets also live on
+    the device, once, for the per-batch gathers."""
+
+    def __init__(self, feats: torch.Tensor, offsets):
+        offsets = [int(o) for o in offsets]
+        if not _offsets_ok(offsets, feats.shape[0]):
+            raise ValueError("VarLenTensor: invalid offsets")
+        self.feats = feats
+        self.offsets = offsets
+        self._dev_offsets: Optional[torch.Tensor] = None
+
+    @staticmethod
+    def offsets_from_seqlen(seqlen):
+        out, start = [0], 0
+        for n in seqlen:
+            start += int(n)
+            out.append(start)
+        return out
+
+    @classmethod
+    def from_tensor_list(cls, tensors) -> "VarLenTensor":
+        return cls(torch.cat(list(tensors), dim=0), cls.offsets_from_seqlen([t.shape[0] for t in tensors]))
+
+    def to_tensor_list(self):
+        return [self.feats[self.offsets[b]:self.offsets[b + 1]] for b in range(self.batch_size())]
+
+    def batch_size(self) -> int:
+        return len(self.offsets) - 1
+
+    __len__ = batch_size
+
+    def shape(self):
+        return [self.batch_size(), *self.feats.shape[1:]]
+
+    def seqlen(self, b: int) -> int:
+        return self.offsets[b + 1] - self.offsets[b]
+
+    def seqlen_list(self):
+        return [self.seqlen(b) for b in range(self.batch_size())]
+
+    def batch_broadcast_map(self):
+        """Row -> batch index, on the host (sparse/basic.mojo:149-155)."""
+        return [b for b in range(self.batch_size()) for _ in range(self.seqlen(b))]
+
+    def device_offsets(self) -> torch.Tensor:
+        if self._dev_offsets is None or self._dev_offsets.device != self.feats.device:
+            self._dev_offsets = torch.tensor(self.offsets, dtype=torch.int64, device=self.feats.device)
+        return self._dev_offsets
+
+    def replace(self, feats: torch.Tensor) -> "VarLenTensor":
+        if feats.shape[0] != self.feats.shape[0]:
+            raise ValueError("VarLenTensor.replace: row count mismatch")
+        out = VarLenTensor.__new__(VarLenTensor)
+        out.feats, out.offsets, out._dev_offsets = feats, self.offsets, self._dev_offsets
+        return out
+
+    def _rows2d(self):
+        f = self.feats.contiguous()
+        t = f.shape[0]
+        return f, f.reshape(t, f.numel() // t if t else 1)
+
+    def elemwise_batch(self, other: torch.Tensor, op: int) -> "VarLenTensor":
+        """feats[r] OP other[b(r)], other [B, row] or [B, 1] (sparse/basic.mojo:204-207)."""
+        if other.shape[0] != self.batch_size():
+            raise ValueError("VarLenTensor.elemwise_batch: batch size mismatch")
+        f, f2 = self._rows2d()
+        oth = other.reshape(other.shape[0], -1).to(device=f.device, dtype=torch.float32).contiguous()
+        return self.replace(ops.binop_rows(f2, oth, op, offsets=self.device_offsets()).reshape(f.shape))
+
+    def elemwise_scalar(self, value: float, op: int, reverse: bool = False) -> "VarLenTensor":
+        """feats OP value (or value OP feats), one f32 rounding (sparse/basic.mojo:201-202)."""
+        f, f2 = self._rows2d()
+        s = torch.full((1, 1), float(value), dtype=torch.float32, device=f.device)
+        return self.replace(ops.binop_rows(f2, s, _REVERSE[op] if reverse else op).reshape(f.shape))
+
+    def __add__(self, other):
+        if isinstance(other, VarLenTensor):
+            if other.feats.numel() != self.feats.numel():
+                raise ValueError("Tensor binop: size mismatch")
+            f, f2 = self._rows2d()
+            _, o2 = other._rows2d()
+            return self.replace(ops.gate_residual(f2, o2).reshape(f.shape))
+        return self.elemwise_scalar(other, OP_ADD)
+
+    def __sub__(self, value: float):
+        return self.elemwise_scalar(value, OP_SUB)
+
+    def __mul__(self, value: float):
+        return self.elemwise_scalar(value, OP_MUL)
+
+    def __truediv__(self, value: float):
+        return self.elemwise_scalar(value, OP_DIV)
+
+    def __neg__(self):
+        return self.elemwise_scalar(-1.0, OP_MUL)
 
 
 class SparseTensor:
@@ -41,6 +151,14 @@ class SparseTensor:
 
     def batch_size(self) -> int:
         return self._batch_size
+
+    @property
+    def vl(self) -> VarLenTensor:
+        """The reference's `x.vl` (feats + offsets, sparse/basic.mojo:296-319);
+        the offsets come to the host once."""
+        v = VarLenTensor(self.feats, self.offsets.cpu().tolist())
+        v._dev_offsets = self.offsets
+        return v
 
     def seqlen(self, b: int) -> int:
         return int(self.offsets[b + 1].item() - self.offsets[b].item())
