@@ -204,6 +204,21 @@ def test_modulation_chunk_views(dev):
     assert_close(got, want, torch.float32, "LN+mod from strided chunks")
 
 
+def test_modulation_linear_path(dev):
+    """Modulation.chunks without share_mod: lin(SiLU(mod)) (modulated.mojo:49-50),
+    the linear a stand-in the device and numpy compute identically
+    (an exact power-of-two scale and a column roll)."""
+    b, c = 3, 256
+    mod = orc.randn(911, (b, c), std=2.0)
+    lin = lambda h: torch.roll(h.repeat(1, 6), 1, dims=1) * 0.5
+    chunks = sparse.Modulation(lin=lin).chunks(to_dev(mod, dev), c)
+    silu = orc.activation(mod, orc.ACT_SILU)
+    want = (np.roll(np.tile(silu, (1, 6)), 1, axis=1) * np.float32(0.5)).astype(np.float32)
+    assert_close(torch.cat(chunks, 1), want, torch.float32, "lin(SiLU(mod)) chunks")
+    with pytest.raises(ValueError, match="not both"):
+        sparse.Modulation()
+
+
 def test_in_place_and_empty(dev):
     x = orc.randn(1001, (64, 1536))
     d = to_dev(x, dev)

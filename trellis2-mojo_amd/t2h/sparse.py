@@ -212,17 +212,28 @@ def gated_residual(x: SparseTensor, h: SparseTensor, gate: torch.Tensor) -> Spar
 
 
 class Modulation:
-    """share_mod path of Modulation.chunks (sparse/transformer/modulated.mojo:24-57):
-    m = mod + modulation (row-broadcast), sliced into the six [N, C] chunks
-    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp. The chunks
-    are strided views of m; every t2h op reads them in place."""
+    """Modulation.chunks (sparse/transformer/modulated.mojo:24-57): the six
+    [N, C] chunks shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp,
+    gate_mlp of m, where m = mod + modulation (share_mod: the [6C] parameter
+    row-broadcast), or m = lin(SiLU(mod)) with `lin` the adaLN linear
+    [C -> 6C] as a callable (a GEMM, outside this library). The chunks are
+    strided views of m; every t2h op reads them in place."""
 
-    def __init__(self, modulation: torch.Tensor):
-        self.share_mod = True
-        self.modulation = modulation.to(torch.float32).contiguous()
+    def __init__(self, modulation: Optional[torch.Tensor] = None, lin=None):
+        if (modulation is None) == (lin is None):
+            raise ValueError("Modulation: give the share_mod parameter or the linear, not both")
+        self.share_mod = modulation is not None
+        self.modulation = modulation.to(torch.float32).contiguous() if modulation is not None else None
+        self.lin = lin
 
     def chunks(self, mod: torch.Tensor, channels: int):
-        m = ops.modulation_add(mod.to(torch.float32).contiguous(), self.modulation)
+        mod = mod.to(torch.float32).contiguous()
+        if self.share_mod:
+            m = ops.modulation_add(mod, self.modulation)
+        else:
+            m = self.lin(ops.activation(mod, ops.ACT_SILU)).to(torch.float32).contiguous()
+        if m.dim() != 2 or m.shape[1] != 6 * channels:
+            raise ValueError("Modulation: expected [N, 6C] modulation rows")
         return [m[:, i * channels:(i + 1) * channels] for i in range(6)]
 
 
