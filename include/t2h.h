@@ -70,6 +70,7 @@ extern "C" {
 #define T2H_ACT_SILU 1
 #define T2H_ACT_GELU 2
 #define T2H_ACT_GELU_TANH 3
+#define T2H_ACT_NONE (-1)        /* t2h_linear: no activation */
 
 /* binary ops: sparse/tensor.mojo:4-7 */
 #define T2H_OP_ADD 0
@@ -229,6 +230,25 @@ int32_t t2h_rope_phases(float* phases_out, int64_t rows, int32_t head_dim,
 int32_t t2h_activation(const void* x, void* out, const float* bias,
                        int64_t rows, int32_t cols, int32_t dtype, int32_t kind,
                        void* stream);
+
+/* ---- weight GEMM on the matrix cores ---------------------------------------
+ * out[t, n] = act(sum_k x[t, k] * w[n, k] + bias[n]): a linear layer with
+ * the bias and activation applied in the GEMM's store.
+ * Replaces: GpuLinear.enqueue_gemm (gpu/linear.mojo:535-560; c[m, co] =
+ * a[m, ci] @ W^T) and, with act = T2H_ACT_GELU_TANH, the MLP's first linear
+ * followed by gelu_tanh_bias (gpu/linear.mojo:662-684, 776-809).
+ * x [rows, in_features] (rows ldx elements apart), w [out_features,
+ * in_features] contiguous (the checkpoint's [out, in] layout), both f16 or
+ * both bf16 (dtype); f32 products and sums, as the reference's 16-bit-weight
+ * kernel gemm_tiled_f16sh (gpu/linear.mojo:326-388). bias [out_features] f32
+ * or NULL; act T2H_ACT_* or T2H_ACT_NONE. out [rows, out_features] (rows ldo
+ * elements apart) in out_dtype = T2H_F32 or dtype.
+ * Shapes: out_features % 256 == 0, in_features % 32 == 0, ldx % 8 == 0,
+ * ldo % 4 == 0; x, w, bias 16-byte aligned. */
+int32_t t2h_linear(const void* x, int64_t ldx, const void* w,
+                   const float* bias, void* out, int64_t ldo, int64_t rows,
+                   int32_t in_features, int32_t out_features, int32_t dtype,
+                   int32_t out_dtype, int32_t act, void* stream);
 
 /* ---- gated residual ------------------------------------------------------
  * Replaces: `y + _gate(h, g)` (modules/transformer/modulated.mojo:22-33,

@@ -423,6 +423,27 @@ void orc_gate(const float* x, const float* g, float* out, int64_t n, int64_t l, 
 /* ------------------------------------------------------------------------ */
 /* pack_q_z / pack_kv_z: gpu/attention.mojo:566-594, 634-662                 */
 /* ------------------------------------------------------------------------ */
+/* gpu/linear.mojo:108-160, 326-388: acc += a[k] * b[k, n] for k in order. The
+ * weight is transposed once so the inner loop runs over n (independent
+ * accumulators, each still summed in k order). */
+void orc_linear(const float* a, const float* w, float* c, int64_t m, int64_t n, int64_t k, int nthreads) {
+    float* wt = (float*)malloc((size_t)(n * k) * sizeof(float));
+    if (wt == NULL) return;
+    for (int64_t j = 0; j < n; ++j)
+        for (int64_t kk = 0; kk < k; ++kk) wt[kk * n + j] = w[j * k + kk];
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int64_t i = 0; i < m; ++i) {
+        float* ci = c + i * n;
+        for (int64_t j = 0; j < n; ++j) ci[j] = 0.0f;
+        for (int64_t kk = 0; kk < k; ++kk) {
+            const float av = a[i * k + kk];
+            const float* wr = wt + kk * n;
+            for (int64_t j = 0; j < n; ++j) ci[j] = ci[j] + av * wr[j];
+        }
+    }
+    free(wt);
+}
+
 void orc_pack_q(const float* qkv, float* qh, int64_t l, int64_t h, int64_t d, int64_t mp, int64_t stride) {
     const float scale = 1.0f / sqrtf((float)d); /* attention.mojo:587 */
     for (int64_t z = 0; z < h; ++z)

@@ -118,6 +118,18 @@ void orc_add_bias(const float* x, const float* bias, float* out,
 void orc_gate(const float* x, const float* g, float* out,
               int64_t n, int64_t l, int64_t c);
 
+/* ---- weight GEMM: gpu/linear.mojo:108-160 (gemm_tiled), 326-388 -------
+ * (gemm_tiled_f16sh). c[m, n] = sum_k a[m, k] * w[n, k], w in the
+ * checkpoint layout [n, k] (GpuLinear uploads W^T, linear.mojo:466-500; the
+ * sum is the same). Each output accumulates its k in increasing order with
+ * one f32 rounding per product and per add, as one thread of the reference
+ * kernel does (its kb/kk loops walk k in order). With 16-bit-valued inputs
+ * (the f16sh kernel rounds both operands to f16) every product is exact.
+ * Rows are independent: OpenMP over rows with nthreads (results do not
+ * depend on nthreads). */
+void orc_linear(const float* a, const float* w, float* c, int64_t m,
+                int64_t n, int64_t k, int nthreads);
+
 /* ---- head-major attention packs: gpu/attention.mojo:566-594, 634-662 -- */
 /* qh [h, mp, d] = q rows (`stride` apart, head z at z*d) * 1/sqrt(f32(d));
  * rows l..mp-1 zero. */

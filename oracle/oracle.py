@@ -411,6 +411,23 @@ def cross_block_resident(x, bk, self_chain, cross_chain, mlp_chain, eps: float =
     return rnd(gate_residual(x, rnd(_f32(mlp_chain(hs))), v(11), bias=v(10)))  # off 10C, gate
 
 
+def linear(a, w, bias=None, act=None, nthreads: int = 8) -> np.ndarray:
+    """act(a @ w^T + bias): gemm_tiled / gemm_tiled_f16sh (gpu/linear.mojo:
+    108-160, 326-388; k summed in order, one f32 rounding per step), then the
+    bias add and activation of gelu_tanh_bias (662-684) / activation
+    (modules/nn.mojo:588-647). a [..., k], w [n, k]."""
+    a, w = _f32(a), _f32(w)
+    k = w.shape[1]
+    a2 = a.reshape(-1, k)
+    out = np.empty((a2.shape[0], w.shape[0]), np.float32)
+    lib().orc_linear(_p(a2), _p(w), _p(out), _i64(a2.shape[0]), _i64(w.shape[0]), _i64(k), int(nthreads))
+    if bias is not None:
+        out = add_bias(out, bias)
+    if act is not None and act >= 0:
+        out = activation(out, act, nthreads)
+    return out.reshape(*a.shape[:-1], w.shape[0])
+
+
 def pack_q(q, l: int, h: int, d: int, mp: int, stride: int) -> np.ndarray:
     """pack_q_z (gpu/attention.mojo:566-594): q rows `stride` apart -> qh
     [h, mp, d] scaled by 1/sqrt(f32(d)), pad rows zero."""

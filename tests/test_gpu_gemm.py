@@ -1,0 +1,97 @@
+"""GPU parity: the MFMA weight GEMM (t2h_linear) against the C oracle's
+restatement of the reference's GEMM (gpu/linear.mojo:108-160, 326-388) with
+the bias add and activation of gelu_tanh_bias (662-684).
+
+Bars:
+- integer-valued operands make every product and partial sum exact, so the
+  GPU's different summation order must still give the oracle's bits;
+- random f16/bf16 operands: both sides sum the same exact products in f32 in
+  different orders, so each output is within 2 * k * 2^-24 * sum|a w| of the
+  oracle (f32 output), and within the storage bar of tests/_parity.py after
+  rounding to f16/bf16.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from _parity import assert_close, host, storage_round, to_dev
+from t2h import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _operands(seed, m, n, k, dtype, std_w=0.02):
+    a = storage_round(orc.randn(seed, (m, k)), dtype)
+    w = storage_round(orc.randn(seed + 1, (n, k), std=std_w), dtype)
+    return a, w
+
+
+def _sum_bound(a, w):
+    return 2.0 * a.shape[1] * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_integer_operands_bit_exact(dev, dtype):
+    """Small-integer operands, ragged rows (300 = 2 token tiles + 44): every
+    output equals the oracle bit for bit; pins the MFMA operand and output
+    lane layouts and the tile bookkeeping."""
+    rng = np.random.default_rng(11)
+    m, n, k = 300, 512, 256
+    a = rng.integers(-6, 7, (m, k)).astype(np.float32)
+    w = rng.integers(-6, 7, (n, k)).astype(np.float32)
+    out = ops.linear(to_dev(a, dev, dtype), to_dev(w, dev, dtype), out_dtype=torch.float32)
+    assert np.array_equal(host(out), orc.linear(a, w))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 129, 1000])
+def test_random_operands_within_sum_bound(dev, dtype, m):
+    n, k = 768, 1536
+    a, w = _operands(1200 + m, m, n, k, dtype)
+    want = orc.linear(a, w)
+    got = host(ops.linear(to_dev(a, dev, dtype), to_dev(w, dev, dtype), out_dtype=torch.float32))
+    assert np.all(np.abs(got - want) <= _sum_bound(a, w))
+    got16 = ops.linear(to_dev(a, dev, dtype), to_dev(w, dev, dtype))
+    assert got16.dtype == dtype
+    assert_close(got16, storage_round(want, dtype), dtype, "linear, 16-bit output")
+
+
+@pytest.mark.parametrize("act", [ops.ACT_NONE, ops.ACT_GELU_TANH, ops.ACT_SILU, ops.ACT_RELU])
+def test_bias_and_activation_epilogue(dev, act):
+    """out = act(fl(acc + bias)): the MLP's first linear with gelu_tanh_bias
+    (and the other activations) in the GEMM's store, f16 output."""
+    m, n, k = 513, 1024, 512
+    a, w = _operands(1300, m, n, k, torch.float16)
+    b = orc.randn(1302, (n,), std=0.02)
+    out = ops.linear(to_dev(a, dev, torch.float16), to_dev(w, dev, torch.float16), bias=to_dev(b, dev), act=act)
+    want = orc.linear(a, w, bias=b, act=act)
+    assert_close(out, want, torch.float16, f"linear act {act}")
+
+
+def test_strided_rows_and_leading_dims(dev):
+    """x rows ldx > k apart (a column slice of a wider buffer) and a [B, L, k]
+    input: the same numbers as the contiguous call."""
+    m, n, k = 200, 256, 128
+    a, w = _operands(1400, m, n, k, torch.float16)
+    wide = torch.zeros((m, k + 64), dtype=torch.float16, device=dev)
+    wide[:, 32:32 + k] = to_dev(a, dev, torch.float16)
+    wd = to_dev(w, dev, torch.float16)
+    got = ops.linear(wide[:, 32:32 + k], wd, out_dtype=torch.float32)
+    ref = ops.linear(to_dev(a, dev, torch.float16), wd, out_dtype=torch.float32)
+    assert torch.equal(got, ref)
+    got3 = ops.linear(to_dev(a, dev, torch.float16).reshape(4, 50, k), wd, out_dtype=torch.float32)
+    assert got3.shape == (4, 50, n) and torch.equal(got3.reshape(m, n), ref)
+
+
+def test_zero_rows_and_shape_errors(dev):
+    w = torch.zeros((256, 64), dtype=torch.float16, device=dev)
+    assert ops.linear(torch.zeros((0, 64), dtype=torch.float16, device=dev), w).shape == (0, 256)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        ops.linear(torch.zeros((4, 64), dtype=torch.float16, device=dev),
+                   torch.zeros((128, 64), dtype=torch.float16, device=dev))
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ops.linear(torch.zeros((4, 40), dtype=torch.float16, device=dev),
+                   torch.zeros((256, 40), dtype=torch.float16, device=dev))
+    with pytest.raises(ValueError, match="f16 or bf16"):
+        ops.linear(torch.zeros((4, 64), device=dev), torch.zeros((256, 64), device=dev))

@@ -454,3 +454,49 @@ def test_flow_schedule_and_sampler_float64():
     for a, b in zip(ts, ts[1:]):
         want = want * (1.0 + (a - b))
     assert np.max(np.abs(out - want) / np.abs(want)) < 1e-5 and len(xs) == 12 and len(x0s) == 12
+
+
+# ---- weight GEMM: gpu/linear.mojo:108-160, 326-388 ---------------------------
+def test_linear_integer_operands_exact():
+    """Small-integer operands: every product and partial sum is an integer
+    below 2^24, so the f32 GEMM is exact in any order and equals numpy's
+    integer matmul. A transposed weight (w [n, k] read as [k, n]) or a dropped
+    k term fails."""
+    rng = np.random.default_rng(5)
+    m, n, k = 37, 24, 40
+    a = rng.integers(-8, 9, (m, k)).astype(np.float32)
+    w = rng.integers(-8, 9, (n, k)).astype(np.float32)
+    want = (a.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    got = orc.linear(a, w, nthreads=3)
+    assert np.array_equal(got, want)
+    assert not np.array_equal(got, (a[:, :-1].astype(np.int64) @ w[:, :-1].astype(np.int64).T).astype(np.float32))
+    sq = rng.integers(-8, 9, (k, k)).astype(np.float32)
+    assert not np.array_equal(orc.linear(a, sq), (a @ sq).astype(np.float32))
+
+
+def test_linear_sums_k_in_order():
+    """Products 2^24, 1, -2^24 summed in k order: fl(fl(2^24 + 1) - 2^24) = 0,
+    while the reverse order gives fl(fl(-2^24 + 1) + 2^24) = 1 (2^24 - 1 is
+    representable). Pins the reference's serial per-thread accumulation."""
+    a = np.array([[1.0, 1.0, 1.0]], np.float32)
+    w = np.array([[2.0 ** 24, 1.0, -(2.0 ** 24)], [-(2.0 ** 24), 1.0, 2.0 ** 24]], np.float32)
+    got = orc.linear(a, w)
+    assert got[0, 0] == 0.0 and got[0, 1] == 1.0
+
+
+def test_linear_float64_bound_bias_and_activation():
+    """f16-valued operands at the DiT's scale: each output is within the
+    serial-sum bound k * 2^-24 * sum|a w| of the float64 product (the
+    products are exact). Bias and GELU-tanh compose as add_bias then
+    activation (act(fl(acc + b)))."""
+    m, n, k = 64, 48, 512
+    a = orc.round_f16(orc.randn(880, (m, k)))
+    w = orc.round_f16(orc.randn(881, (n, k), std=0.02))
+    b = orc.randn(882, (n,), std=0.02)
+    got = orc.linear(a, w)
+    exact = a.astype(np.float64) @ w.astype(np.float64).T
+    bound = k * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.max(np.abs(got - exact)) > 0.0      # f32 sums do round
+    full = orc.linear(a, w, bias=b, act=orc.ACT_GELU_TANH)
+    assert np.array_equal(full, orc.activation(orc.add_bias(got, b), orc.ACT_GELU_TANH))

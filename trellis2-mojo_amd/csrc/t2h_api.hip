@@ -477,6 +477,43 @@ int32_t t2h_activation(const void* x, void* out, const float* bias, int64_t rows
     return hip_status(launch_activation(a, static_cast<hipStream_t>(stream)), fn);
 }
 
+int32_t t2h_linear(const void* x, int64_t ldx, const void* w, const float* bias, void* out, int64_t ldo, int64_t rows,
+                   int32_t in_features, int32_t out_features, int32_t dtype, int32_t out_dtype, int32_t act,
+                   void* stream) {
+    const char* fn = "t2h_linear";
+    if (dtype != T2H_F16 && dtype != T2H_BF16) return fail(T2H_EINVAL, "%s: operands must be f16 or bf16", fn);
+    if (out_dtype != T2H_F32 && out_dtype != dtype)
+        return fail(T2H_EINVAL, "%s: out_dtype must be f32 or the operand dtype", fn);
+    if (act != T2H_ACT_NONE && (act < T2H_ACT_RELU || act > T2H_ACT_GELU_TANH))
+        return fail(T2H_EINVAL, "unknown activation");
+    if (rows < 0 || in_features <= 0 || out_features <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
+    if (out_features % gemm_feature_tile() != 0)
+        return fail(T2H_EINVAL, "%s: out_features %d is not a multiple of %d", fn, out_features, gemm_feature_tile());
+    if (in_features % gemm_k_step() != 0)
+        return fail(T2H_EINVAL, "%s: in_features %d is not a multiple of %d", fn, in_features, gemm_k_step());
+    if (ldx < in_features || ldo < out_features) return fail(T2H_EINVAL, "%s: row stride below the row", fn);
+    if (ldx % 8 != 0 || ldo % 4 != 0) return fail(T2H_EINVAL, "%s: ldx must be a multiple of 8, ldo of 4", fn);
+    if (rows == 0) return ok();
+    if (x == nullptr || w == nullptr || out == nullptr) return fail(T2H_EINVAL, "%s: NULL tensor", fn);
+    if (!aligned(x, 16) || !aligned(w, 16) || (bias != nullptr && !aligned(bias, 16)) ||
+        !aligned(out, out_dtype == T2H_F32 ? 16 : 8))
+        return fail(T2H_EINVAL, "%s: misaligned tensor", fn);
+    GemmArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.w = w;
+    a.rows = rows;
+    a.n = out_features;
+    a.k = in_features;
+    a.dtype = dtype;
+    a.bias = bias;
+    a.act = act;
+    a.out = out;
+    a.ldo = ldo;
+    a.out_dtype = out_dtype;
+    return hip_status(launch_gemm(a, static_cast<hipStream_t>(stream)), fn);
+}
+
 int32_t t2h_gate_residual(const void* x, const void* h, void* out, const float* bias, const float* gate,
                           int64_t p_stride, int64_t rows, int32_t cols, int32_t dtype, const int64_t* offsets,
                           int32_t nbatch, int64_t rows_per_batch, void* stream) {

@@ -102,6 +102,26 @@ struct PackArgs {
     int32_t k_transposed;
 };
 
+// Weight GEMM on MFMA (t2h_linear, t2h_qkv_linear_pack):
+// acc[t, n] = sum_k x[t, k] * w[n, k], f16/bf16 operands, f32 accumulation,
+// then an epilogue in the store (bias + activation, or the attention pack).
+struct GemmArgs {
+    const void* x;           // [rows, k], rows ldx elements apart
+    int64_t ldx;
+    const void* w;           // [n, k] contiguous (a linear's [out, in] weight)
+    int64_t rows;
+    int32_t n;               // output features, a multiple of the feature tile
+    int32_t k;               // input features, a multiple of the k step
+    int32_t dtype;           // operand storage: T2H_F16 / T2H_BF16
+    const float* bias;       // [n] f32 or nullptr
+    int32_t act;             // T2H_ACT_* or -1 (none)
+    void* out;               // [rows, n], rows ldo elements apart
+    int64_t ldo;
+    int32_t out_dtype;       // T2H_F32 or dtype
+    int64_t nblocks;         // set by the launcher: token tiles x feature tiles
+    int32_t ftiles;          // feature tiles
+};
+
 // Flow-matching Euler step (t2h_flow_euler_step).
 constexpr int kEulerChunk = 4096;   // elements per block
 constexpr int kEulerMaxSeg = 64;    // varlen segments carried in the kernel arguments
@@ -171,6 +191,11 @@ hipError_t launch_ln(const LnArgs& a, hipStream_t s);
 hipError_t launch_qk(const QkArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_phases(const PhaseArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_pack(const PackArgs& a, const RopeSlots& tab, hipStream_t s);
+// t2h_gemm.hip
+hipError_t launch_gemm(GemmArgs a, hipStream_t s);
+int32_t gemm_feature_tile();   // output features per block (out_features must be a multiple)
+int32_t gemm_k_step();         // k per stage (in_features must be a multiple)
+// t2h_sampler.hip
 hipError_t launch_euler(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
 // t2h_eltwise.hip
 hipError_t launch_activation(const EltArgs& a, hipStream_t s);

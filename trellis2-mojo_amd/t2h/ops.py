@@ -19,6 +19,7 @@ from ._lib import BF16, F16, F32, LN_AFFINE, LN_MODULATE, LN_PLAIN, call
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 ACT_RELU, ACT_SILU, ACT_GELU, ACT_GELU_TANH = 0, 1, 2, 3
+ACT_NONE = -1
 OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_RSUB, OP_RDIV = 0, 1, 2, 3, 4, 5
 
 
@@ -334,6 +335,35 @@ def activation(x, kind: int = ACT_GELU_TANH, bias=None, out=None) -> torch.Tenso
     bp, _, _ = _param_rows(bias, c, "activation")
     out = torch.empty_like(x) if out is None else out
     call("t2h_activation", x.data_ptr(), out.data_ptr(), bp, rows, c, dt, int(kind), _stream())
+    return out
+
+
+def linear(x, weight, bias=None, act: int = ACT_NONE, out_dtype=None, out=None) -> torch.Tensor:
+    """act(x @ weight^T + bias) on the matrix cores: x [..., K] (rows may be
+    strided, unit column stride), weight [N, K] contiguous, both float16 or
+    both bfloat16; bias [N] float32 or None; f32 sums; out [..., N] in
+    out_dtype (float32 or x's dtype, default x's)."""
+    _dev(x, "linear")
+    _dev(weight, "linear")
+    dt = _dtype(x, "linear")
+    if weight.dtype != x.dtype or weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("linear: weight must be a contiguous [N, K] tensor of x's dtype")
+    n, k = weight.shape
+    if x.shape[-1] != k or x.stride(-1) != 1:
+        raise ValueError("linear: x's last dim must be K with unit stride")
+    x2 = x.reshape(-1, k) if x.dim() != 2 else x
+    rows, ldx = x2.shape[0], (x2.stride(0) if x2.shape[0] > 1 else k)
+    if bias is not None:
+        _dev(bias, "linear")
+        if bias.dtype != torch.float32 or bias.numel() != n or not bias.is_contiguous():
+            raise ValueError("linear: bias must be a contiguous float32 [N] tensor")
+    od = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((*x.shape[:-1], n), dtype=od, device=x.device)
+    elif out.dtype != od or out.shape != (*x.shape[:-1], n) or not out.is_contiguous():
+        raise ValueError("linear: out must be a contiguous [..., N] tensor of out_dtype")
+    call("t2h_linear", x2.data_ptr(), ldx, weight.data_ptr(), bias.data_ptr() if bias is not None else None,
+         out.data_ptr(), n, rows, k, n, dt, _dtype(out, "linear"), int(act), _stream())
     return out
 
 
