@@ -50,7 +50,9 @@ def build(verbose: bool = False) -> str:
         futs = [ex.submit(_run, [HIPCC, *CFLAGS, "-c", s, "-o", o]) for s, o in zip(sources, objs)]
         logs = [f.result() for f in futs]
     tmp = LIB_PATH + ".tmp"
-    logs.append(_run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]))
+    # -z defs: an unresolved symbol (e.g. a kernel whose host stub was not
+    # emitted) fails the link here instead of the first dlopen on a GPU box
+    logs.append(_run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *objs, "-o", tmp]))
     os.replace(tmp, LIB_PATH)
     if verbose:
         print("\n".join(l for l in logs if l.strip()))
