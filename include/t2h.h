@@ -202,6 +202,31 @@ int32_t t2h_attn_pack(const void* q, const void* k, const void* v,
                       int64_t mp, void* k_out, void* vh, int64_t lp,
                       int32_t k_transposed, void* stream);
 
+/* ---- qkv linear fused with the attention epilogue and head-major pack -----
+ * The self-attention chain's qkv GEMM, bias_rms_rope_qkv, pack_q_z and
+ * pack_kv_z in one kernel: the GEMM's [rows, 3, H, D] output stays in
+ * registers and only the packed operands are written.
+ * Replaces: GpuLinear.enqueue_gemm of the qkv linear followed by
+ * bias_rms_rope_qkv + pack_q_z + pack_kv_z (gpu/attention.mojo:983-1013;
+ * kernels 507-563, 566-594, 634-662; gpu/linear.mojo:535-560).
+ * x [rows, in_features] (rows ldx elements apart) and w [3*heads*head_dim,
+ * in_features] (the qkv linear's [out, in] weight), both f16 or both bf16,
+ * f32 sums. Biases, gammas, RoPE sources and outputs as t2h_attn_pack; all
+ * three outputs are required. head_dim must be 128 and heads even;
+ * in_features % 64 == 0. */
+int32_t t2h_qkv_linear_pack(const void* x, int64_t ldx, const void* w,
+                            int64_t rows, int32_t in_features, int32_t heads,
+                            int32_t head_dim, int32_t dtype,
+                            const float* bias_q, const float* bias_k,
+                            const float* bias_v, const float* gamma_q,
+                            const float* gamma_k, int32_t use_rope,
+                            const float* freqs_host, int32_t freq_dim,
+                            int32_t pos_dim, const float* phases,
+                            int64_t phase_rows, const int32_t* coords,
+                            int32_t coord_cols, int32_t grid_res, void* qh,
+                            int64_t mp, void* k_out, void* vh, int64_t lp,
+                            int32_t k_transposed, void* stream);
+
 /* Host function (no device work): the embedders' frequency table
  * freqs[j] = f32(freq_lo) / f32(freq_hi) ** (f32(j) / f32(freq_dim)),
  * freq_dim = head_dim / 2 / dim, in f32 with libm powf — the constructor of
@@ -243,8 +268,9 @@ int32_t t2h_activation(const void* x, void* out, const float* bias,
  * kernel gemm_tiled_f16sh (gpu/linear.mojo:326-388). bias [out_features] f32
  * or NULL; act T2H_ACT_* or T2H_ACT_NONE. out [rows, out_features] (rows ldo
  * elements apart) in out_dtype = T2H_F32 or dtype.
- * Shapes: out_features % 256 == 0, in_features % 32 == 0, ldx % 8 == 0,
- * ldo % 4 == 0; x, w, bias 16-byte aligned. */
+ * Shapes: out_features % 256 == 0, in_features % 64 == 0, ldx % 8 == 0,
+ * ldo % 8 (16-bit out) or % 4 (f32 out) == 0; x, w, bias, out 16-byte
+ * aligned. */
 int32_t t2h_linear(const void* x, int64_t ldx, const void* w,
                    const float* bias, void* out, int64_t ldo, int64_t rows,
                    int32_t in_features, int32_t out_features, int32_t dtype,

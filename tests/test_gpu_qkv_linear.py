@@ -1,0 +1,138 @@
+"""GPU parity: the qkv linear fused with the self-attention epilogue and the
+head-major pack (t2h_qkv_linear_pack), through the C ABI, against the C
+oracle's composition of the reference's chain: the qkv GEMM
+(gpu/linear.mojo:326-388, f16 operands, f32 sums), bias_rms_rope_qkv,
+pack_q_z and pack_kv_z (gpu/attention.mojo:507-563, 566-594, 634-662, order
+983-1013).
+
+Bar: the f16 (bf16) storage tolerance of tests/_parity.py. The GEMM sums the
+same exact products in another order and the head's sum of squares is
+reduced in another order, both far below the storage rounding; pads are
+exact zeros."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from _parity import assert_close, host, storage_round, to_dev
+from t2h import nn, ops, workloads
+from t2h._lib import T2HError
+
+pytestmark = pytest.mark.gpu
+H, D, C = 12, 128, 1536
+
+
+def _case(seed, rows, dtype, k=C):
+    x = storage_round(orc.randn(seed, (rows, k)), dtype)
+    w = storage_round(orc.randn(seed + 1, (3 * H * D, k), std=0.02), dtype)
+    bias = orc.randn(seed + 2, (3 * H * D,), std=0.05)
+    gq = orc.randn(seed + 3, (H, D), mean=1.0, std=0.02)
+    gk = orc.randn(seed + 4, (H, D), mean=1.0, std=0.02)
+    return x, w, bias, gq, gk
+
+
+def _want(x, w, bias, gq, gk, phases, mp, lp):
+    qkv = orc.linear(x, w)
+    return orc.attn_pack(qkv, H, D, mp, lp, bias, gq, gk, phases)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_sparse_coords_padded(dev, dtype):
+    """Config-4 voxel rows (the first 3000 of the 64^3 shells) with RoPE from
+    int coords, padded to a multiple of 64 as the reference chain does."""
+    coords, _ = workloads.config4()
+    coords = np.ascontiguousarray(coords[:3000])
+    rows = coords.shape[0]
+    mp = (rows + 63) // 64 * 64
+    x, w, bias, gq, gk = _case(5000, rows, dtype)
+    phases = orc.rope_phases_from_coords(coords, D, orc.rope_freqs(D))
+    wq, wk, wv = _want(x, w, bias, gq, gk, phases, mp, mp)
+    qh, kt, vh = ops.qkv_linear_pack(to_dev(x, dev, dtype), to_dev(w, dev, dtype), H, bias=to_dev(bias, dev),
+                                     gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), mp=mp, lp=mp,
+                                     freqs=nn.rope_freqs(D), coords=to_dev(coords, dev))
+    assert qh.shape == (H, mp, D) and kt.shape == (H, D, mp) and vh.shape == (H, mp, D)
+    assert_close(qh, wq, dtype, "qh")
+    assert_close(kt, wk, dtype, "kt")
+    assert_close(vh, wv, dtype, "vh")
+    assert not host(qh)[:, rows:].any() and not host(kt)[:, :, rows:].any() and not host(vh)[:, rows:].any()
+
+
+def test_dense_grid_phase_table_and_k_layouts(dev):
+    """Config-2 tokens (16^3 grid, 4096 rows) with the reference's uploaded
+    phase table; k row-major [H, lp, D] is the transpose of the [H, D, lp] k."""
+    rows = 4096
+    x, w, bias, gq, gk = _case(5100, rows, torch.float16)
+    phases = orc.rope_phases_from_positions(orc.grid_positions(16), D, orc.rope_freqs(D))
+    wq, wk, wv = _want(x, w, bias, gq, gk, phases, rows, rows)
+    args = dict(bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(D),
+                phases=to_dev(phases, dev))
+    xd, wd = to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16)
+    qh, kt, vh = ops.qkv_linear_pack(xd, wd, H, **args)
+    assert_close(qh, wq, torch.float16, "qh")
+    assert_close(kt, wk, torch.float16, "kt")
+    assert_close(vh, wv, torch.float16, "vh")
+    qh2, kr, vh2 = ops.qkv_linear_pack(xd, wd, H, k_transposed=False, **args)
+    assert torch.equal(qh2, qh) and torch.equal(vh2, vh)
+    assert torch.equal(kr, kt.transpose(1, 2).contiguous())
+
+
+def test_grid_positions_match_phase_table(dev):
+    """Positions from the dense grid index (no table) give the result of a
+    phase table built on the device from the same grid (same sincos)."""
+    rows = 1000
+    x, w, bias, gq, gk = _case(5200, rows, torch.float16)
+    xd, wd = to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16)
+    phases = ops.rope_phases(rows, D, nn.rope_freqs(D), grid_res=16, device=dev)
+    kw = dict(bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(D))
+    a = ops.qkv_linear_pack(xd, wd, H, grid_res=16, **kw)
+    b = ops.qkv_linear_pack(xd, wd, H, phases=phases, **kw)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_no_rms_no_rope_no_bias_is_gemm_plus_pack(dev):
+    """Without bias, RMS and RoPE the op is the GEMM followed by the packs:
+    every output equals t2h_linear's f32 sums rounded once, permuted (bit
+    exact), q scaled by 1/sqrt(D) in f32."""
+    rows = 700
+    x, w, _, _, _ = _case(5300, rows, torch.float16)
+    xd, wd = to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16)
+    qh, kt, vh = ops.qkv_linear_pack(xd, wd, H, use_rope=False, mp=768, lp=768)
+    qkv = host(ops.linear(xd, wd, out_dtype=torch.float32)).reshape(rows, 3, H, D)
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    assert np.array_equal(host(qh)[:, :rows], storage_round((qkv[:, 0] * scale).transpose(1, 0, 2), torch.float16))
+    assert np.array_equal(host(kt)[:, :, :rows], storage_round(qkv[:, 1].transpose(1, 2, 0), torch.float16))
+    assert np.array_equal(host(vh)[:, :rows], storage_round(qkv[:, 2].transpose(1, 0, 2), torch.float16))
+    assert not host(qh)[:, rows:].any() and not host(vh)[:, rows:].any()
+
+
+def test_pads_beyond_the_last_token_tile(dev):
+    """mp and lp past the token tiles of the rows (rows = 300, pads to 1000):
+    tiles with no rows skip the GEMM and write zeros; mp != lp."""
+    rows = 300
+    x, w, bias, gq, gk = _case(5400, rows, torch.float16)
+    phases = orc.rope_phases_from_positions(orc.grid_positions(16)[:rows], D, orc.rope_freqs(D))
+    wq, wk, wv = _want(x, w, bias, gq, gk, phases, 1000, 1024)
+    qh, kt, vh = ops.qkv_linear_pack(to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16), H,
+                                     bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev),
+                                     mp=1000, lp=1024, freqs=nn.rope_freqs(D), phases=to_dev(phases, dev))
+    assert qh.shape == (H, 1000, D) and kt.shape == (H, D, 1024)
+    assert_close(qh, wq, torch.float16, "qh")
+    assert_close(kt, wk, torch.float16, "kt")
+    assert_close(vh, wv, torch.float16, "vh")
+
+
+def test_zero_rows_and_errors(dev):
+    w = torch.zeros((3 * H * D, C), dtype=torch.float16, device=dev)
+    qh, kt, vh = ops.qkv_linear_pack(torch.zeros((0, C), dtype=torch.float16, device=dev), w, H, mp=64, lp=64,
+                                     use_rope=False)
+    assert not host(qh).any() and not host(kt).any() and not host(vh).any()
+    with pytest.raises(T2HError, match="head_dim must be 128"):
+        ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev),
+                            torch.zeros((3 * H * 64, C), dtype=torch.float16, device=dev), H, use_rope=False)
+    with pytest.raises(T2HError, match="even heads"):
+        ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev),
+                            torch.zeros((3 * 3 * D, C), dtype=torch.float16, device=dev), 3, use_rope=False)
+    with pytest.raises(ValueError, match="lp % 8"):
+        ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev), w, H, mp=4, lp=4,
+                            use_rope=False)

@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <cstdint>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -421,6 +422,78 @@ int32_t t2h_attn_pack(const void* q, const void* k, const void* v, int64_t in_st
     return hip_status(launch_pack(a, tab, static_cast<hipStream_t>(stream)), fn);
 }
 
+int32_t t2h_qkv_linear_pack(const void* x, int64_t ldx, const void* w, int64_t rows, int32_t in_features,
+                            int32_t heads, int32_t head_dim, int32_t dtype, const float* bias_q, const float* bias_k,
+                            const float* bias_v, const float* gamma_q, const float* gamma_k, int32_t use_rope,
+                            const float* freqs_host, int32_t freq_dim, int32_t pos_dim, const float* phases,
+                            int64_t phase_rows, const int32_t* coords, int32_t coord_cols, int32_t grid_res,
+                            void* qh, int64_t mp, void* k_out, void* vh, int64_t lp, int32_t k_transposed,
+                            void* stream) {
+    const char* fn = "t2h_qkv_linear_pack";
+    if (dtype != T2H_F16 && dtype != T2H_BF16) return fail(T2H_EINVAL, "%s: operands must be f16 or bf16", fn);
+    if (rows < 0 || heads <= 0 || heads > 65535 || in_features <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
+    if (head_dim != gemm_head_dim())
+        return fail(T2H_EUNSUPPORTED, "%s: head_dim must be %d", fn, gemm_head_dim());
+    const int64_t n = 3 * (int64_t)heads * head_dim;
+    if (n % gemm_feature_tile() != 0 || n > INT32_MAX)
+        return fail(T2H_EUNSUPPORTED, "%s: 3 * heads * head_dim must be a multiple of %d (even heads)", fn,
+                    gemm_feature_tile());
+    if (in_features % gemm_k_step() != 0)
+        return fail(T2H_EINVAL, "%s: in_features %d is not a multiple of %d", fn, in_features, gemm_k_step());
+    if (ldx < in_features || ldx % 8 != 0) return fail(T2H_EINVAL, "%s: ldx must be >= in_features and a multiple of 8", fn);
+    if (qh == nullptr || k_out == nullptr || vh == nullptr) return fail(T2H_EINVAL, "%s: NULL output", fn);
+    if (mp < rows || lp < rows) return fail(T2H_EINVAL, "%s: mp and lp must be >= rows", fn);
+    if (k_transposed && lp % 8 != 0) return fail(T2H_EINVAL, "%s: transposed k needs lp %% 8 == 0", fn);
+    if ((gamma_q == nullptr) != (gamma_k == nullptr))
+        return fail(T2H_EINVAL, "%s: gamma_q and gamma_k must both be given or both NULL", fn);
+    RopeSlots tab;
+    std::memset(&tab, 0, sizeof(tab));
+    if (use_rope) {
+        if (int32_t rc = build_slots(head_dim, freqs_host, freq_dim, pos_dim, tab, fn)) return rc;
+        if (int32_t rc = check_positions(phases, phase_rows, coords, coord_cols, grid_res, pos_dim, fn)) return rc;
+    }
+    if (rows > 0 && (x == nullptr || w == nullptr)) return fail(T2H_EINVAL, "%s: NULL input", fn);
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(qh, 16) || !aligned(k_out, 16) || !aligned(vh, 16) ||
+        !aligned(bias_q, 16) || !aligned(bias_k, 16) || !aligned(bias_v, 16) || !aligned(gamma_q, 16) ||
+        !aligned(gamma_k, 16) || !aligned(phases, 16))
+        return fail(T2H_EINVAL, "%s: tensors and f32 parameters must be 16-byte aligned", fn);
+    if (mp == 0 && lp == 0) return ok();
+    GemmArgs g{};
+    g.x = x;
+    g.ldx = ldx;
+    g.w = w;
+    g.rows = rows;
+    g.n = (int32_t)n;
+    g.k = in_features;
+    g.dtype = dtype;
+    PackArgs a{};
+    a.rows = rows;
+    a.heads = heads;
+    a.head_dim = head_dim;
+    a.dtype = dtype;
+    a.bias_q = bias_q;
+    a.bias_k = bias_k;
+    a.bias_v = bias_v;
+    a.gamma_q = gamma_q;
+    a.gamma_k = gamma_k;
+    a.rms_scale = std::sqrt((float)head_dim);           // sqrt(Float32(d)), attention.mojo:539
+    a.q_scale = 1.0f / std::sqrt((float)head_dim);      // attention.mojo:587
+    a.use_rope = use_rope ? 1 : 0;
+    a.pos_dim = pos_dim;
+    a.phases = use_rope ? phases : nullptr;
+    a.phase_rows = phase_rows;
+    a.coords = (use_rope && phases == nullptr) ? coords : nullptr;
+    a.coord_cols = coord_cols;
+    a.grid_res = grid_res;
+    a.qh = qh;
+    a.mp = mp;
+    a.k_out = k_out;
+    a.vh = vh;
+    a.lp = lp;
+    a.k_transposed = k_transposed ? 1 : 0;
+    return hip_status(launch_qkv_pack(g, a, tab, static_cast<hipStream_t>(stream)), fn);
+}
+
 int32_t t2h_rope_freqs(int32_t head_dim, int32_t dim, double freq_lo, double freq_hi, float* freqs_host,
                        int32_t capacity) {
     if (head_dim <= 0 || head_dim % 2 != 0)
@@ -492,11 +565,12 @@ int32_t t2h_linear(const void* x, int64_t ldx, const void* w, const float* bias,
     if (in_features % gemm_k_step() != 0)
         return fail(T2H_EINVAL, "%s: in_features %d is not a multiple of %d", fn, in_features, gemm_k_step());
     if (ldx < in_features || ldo < out_features) return fail(T2H_EINVAL, "%s: row stride below the row", fn);
-    if (ldx % 8 != 0 || ldo % 4 != 0) return fail(T2H_EINVAL, "%s: ldx must be a multiple of 8, ldo of 4", fn);
+    if (ldx % 8 != 0 || ldo % (out_dtype == T2H_F32 ? 4 : 8) != 0)
+        return fail(T2H_EINVAL, "%s: ldx must be a multiple of 8, ldo of %d", fn, out_dtype == T2H_F32 ? 4 : 8);
     if (rows == 0) return ok();
     if (x == nullptr || w == nullptr || out == nullptr) return fail(T2H_EINVAL, "%s: NULL tensor", fn);
     if (!aligned(x, 16) || !aligned(w, 16) || (bias != nullptr && !aligned(bias, 16)) ||
-        !aligned(out, out_dtype == T2H_F32 ? 16 : 8))
+        !aligned(out, 16))
         return fail(T2H_EINVAL, "%s: misaligned tensor", fn);
     GemmArgs a{};
     a.x = x;

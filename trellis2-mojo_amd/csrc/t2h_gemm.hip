@@ -33,6 +33,7 @@
 #include "t2h_device.h"
 #include "t2h_internal.h"
 #include "t2h_act.h"
+#include "t2h_rope.h"
 
 namespace t2h {
 namespace {
@@ -192,26 +193,33 @@ __device__ __forceinline__ float epi_f(float acc, float b) {
     else return act_f<ACT>(v);
 }
 
-template <typename T, typename O, int ACT>
-__global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmArgs a) {
+// Block tile of a launch: token tile t0 and feature tile n0 of block b.
+struct TileOf {
+    int64_t t0, n0;
+    __device__ __forceinline__ bool init(const GemmArgs& a) {
+        const int64_t b = block_linear();
+        if (b >= a.nblocks) return false;
+        const int64_t u = xcd_tile(b, a.nblocks);
+        const int64_t tt = u / a.ftiles;
+        t0 = tt * kBT;
+        n0 = (u - tt * a.ftiles) * kBF;
+        return true;
+    }
+};
+
+// The block's accumulators acc[t0.., n0..] over all of k. On return every
+// wave has finished reading the LDS stages (a barrier follows the last one),
+// so the caller may reuse the LDS.
+template <typename T>
+__device__ __forceinline__ void gemm_mainloop(const GemmArgs& a, int64_t t0, int64_t n0, uint8_t* lds,
+                                              f32x16 (&acc)[kFI][kTJ]) {
     using V8 = typename Mfma<T>::v8;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
-
-    const int64_t b = block_linear();
-    if (b >= a.nblocks) return;
-    const int64_t u = xcd_tile(b, a.nblocks);
-    const int64_t tt = u / a.ftiles;
-    const int ft = (int)(u - tt * a.ftiles);
-    const int64_t t0 = tt * kBT;
-    const int64_t n0 = (int64_t)ft * kBF;
-
+    static_assert(sizeof(T) == 2, "16-bit operands");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wf = wave & 1;
     const int wt = wave >> 1;
-
-    static_assert(sizeof(T) == 2, "16-bit operands");
     const uint8_t* wbase = static_cast<const uint8_t*>(a.w) + n0 * (int64_t)a.k * 2;
     const uint8_t* xbase = static_cast<const uint8_t*>(a.x) + t0 * a.ldx * 2;
     const int64_t tlast = a.rows - 1 - t0;   // last valid token row of the tile
@@ -234,14 +242,6 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
             src[i] = (tr * a.ldx + kc * 8) * 2;
         }
     }
-
-    f32x16 acc[kFI][kTJ];
-#pragma unroll
-    for (int fi = 0; fi < kFI; ++fi)
-#pragma unroll
-        for (int tj = 0; tj < kTJ; ++tj)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[fi][tj][r] = 0.0f;
 
     // fragment slots: row lane % 32 of each MFMA tile, k chunk 2s + lane / 32;
     // (2s | h) ^ swz = (h ^ swz) ^ 2s, so substep s's slot is slot ^ 32s
@@ -278,27 +278,328 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
     for (; ks + 2 < ksteps; ++ks) stage_body<T, true, true>(acc, af, bf, cx, ks);
     if (ks + 1 < ksteps) stage_body<T, true, false>(acc, af, bf, cx, ks++);
     stage_body<T, false, false>(acc, af, bf, cx, ks);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();                // every wave is done reading the stages
+}
 
-    // epilogue: lane holds token t of each token tile and features
-    // n + 8q + 4(lane / 32) + 0..3 of each feature tile
-    O* __restrict__ out = static_cast<O*>(a.out);
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[kFI][kTJ]) {
 #pragma unroll
-    for (int tj = 0; tj < kTJ; ++tj) {
-        const int64_t t = t0 + wt * kWT + tj * 32 + fr;
-        if (t >= a.rows) continue;
+    for (int fi = 0; fi < kFI; ++fi)
+#pragma unroll
+        for (int tj = 0; tj < kTJ; ++tj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fi][tj][r] = 0.0f;
+}
+
+// ---- linear: out = act(acc + bias) ------------------------------------------
+// The lane holds token wt*kWT + tj*32 + fr of each token tile and features
+// wf*kWF + fi*32 + 8q + 4h + 0..3. bias + activation are applied in f32 on
+// the accumulators (one rounding to the output type). 16-bit outputs are
+// staged in LDS as 256 token rows of 512 bytes (16-byte chunk c of row r at
+// c ^ (r % 32): conflict-free both ways) and leave as whole rows, 16
+// contiguous bytes per lane; f32 outputs go out directly.
+template <typename T, typename O, int ACT>
+__global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+    TileOf tile;
+    if (!tile.init(a)) return;
+    const int64_t t0 = tile.t0, n0 = tile.n0;
+    f32x16 acc[kFI][kTJ];
+    zero_acc(acc);
+    gemm_mainloop<T>(a, t0, n0, lds, acc);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wf = wave & 1, wt = wave >> 1;
+    const int fr = lane & 31, h = lane >> 5;
+    O* __restrict__ out = static_cast<O*>(a.out);
+    auto bias4 = [&](int fi, int q, float* bq) {
+        if (a.bias != nullptr) {
+            load_params<4>(a.bias + n0 + wf * kWF + fi * 32 + q * 8 + h * 4, bq);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bq[i] = 0.0f;
+        }
+    };
+    if constexpr (sizeof(O) == 2) {
+        static_assert(kBT * kBF * 2 <= kStages * kStageBytes, "C tile fits the stage buffers");
 #pragma unroll
         for (int fi = 0; fi < kFI; ++fi) {
+            float bv[4][4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t n = n0 + wf * kWF + fi * 32 + q * 8 + h * 4;
-                float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (a.bias != nullptr) load_params<4>(a.bias + n, bv);
-                float v[4];
+            for (int q = 0; q < 4; ++q) bias4(fi, q, bv[q]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = epi_f<ACT>(acc[fi][tj][q * 4 + i], bv[i]);
-                store_elems<O, 4>(out + t * a.ldo + n, v);
+            for (int tj = 0; tj < kTJ; ++tj) {
+                const int r = wt * kWT + tj * 32 + fr;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = (wf * kWF + fi * 32 + q * 8) / 8;
+                    float v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = epi_f<ACT>(acc[fi][tj][q * 4 + i], bv[q][i]);
+                    u32x2 w;
+                    w.x = Word<O>::pack(v);
+                    w.y = Word<O>::pack(v + 2);
+                    *reinterpret_cast<u32x2*>(lds + r * (kBF * 2) + ((c ^ (r & 31)) * 16) + h * 8) = w;
+                }
             }
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        constexpr int kRowsPerWave = kBT / 4;
+#pragma unroll 4
+        for (int it = 0; it < kRowsPerWave / 2; ++it) {
+            const int r = wave * kRowsPerWave + it * 2 + h;
+            const int c = fr;
+            const int64_t t = t0 + r;
+            const u32x4 w = *reinterpret_cast<const u32x4*>(lds + r * (kBF * 2) + ((c ^ (r & 31)) * 16));
+            if (t < a.rows) *reinterpret_cast<u32x4*>(out + t * a.ldo + n0 + c * 8) = w;
+        }
+    } else {
+#pragma unroll
+        for (int fi = 0; fi < kFI; ++fi) {
+            float bv[4][4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bias4(fi, q, bv[q]);
+#pragma unroll
+            for (int tj = 0; tj < kTJ; ++tj) {
+                const int64_t t = t0 + wt * kWT + tj * 32 + fr;
+                if (t >= a.rows) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t n = n0 + wf * kWF + fi * 32 + q * 8 + h * 4;
+                    float v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = epi_f<ACT>(acc[fi][tj][q * 4 + i], bv[q][i]);
+                    store_elems<O, 4>(out + t * a.ldo + n, v);
+                }
+            }
+        }
+    }
+}
+
+// ---- qkv linear + attention epilogue + head-major pack ----------------------
+// The qkv GEMM's output [rows, 3, H, 128] never reaches memory. A wave's 128
+// features are one head (q, k or v: head hg = n / 128, tensor hg / H, head
+// hg % H) for 128 tokens, and each token's head lives in two lanes (l and
+// l ^ 32, 64 values each). Per token, in the order of the separate kernels
+// (bias_rms_rope_qkv, pack_q_z, pack_kv_z): + bias; q/k: RMS over the head,
+// x * rsqrt(sum x^2) * (gamma * sqrt(D)); q/k: RoPE on the in-lane pairs
+// (2p, 2p + 1) with cos/sin from the phase table or from the token's
+// position; q: * 1/sqrt(D); tokens >= rows: 0. The head then goes through
+// the wave's own 16 KB of LDS, 64 tokens at a time, as 256-byte token rows
+// and leaves as 16-byte vectors: whole token rows (qh [H, mp, D], k [H, lp,
+// D], vh [H, lp, D]) or, for the transposed k [H, D, lp], 8 tokens of one
+// feature gathered from 8 rows. Tiles past the last token row skip the GEMM
+// and write the pads.
+constexpr int kHead = 128;
+static_assert(kTJ == 4, "copy_col cases");
+
+// Slot of a 16-byte chunk in a staged 256-byte token row: chunk c of row r
+// at c ^ stage_swz(r). Over 32 consecutive rows (one row-major write) every
+// slot appears twice; over rows 8g + j, g = 0..7 (one transposed gather)
+// the slots are distinct; a row's 16 chunks are a permutation.
+__device__ __forceinline__ int stage_swz(int r) { return ((r >> 3) ^ ((r & 7) << 1)) & 15; }
+
+template <int TJ>
+__device__ __forceinline__ void copy_col(const f32x16 (&acc)[kFI][kTJ], float (&col)[kFI][16]) {
+#pragma unroll
+    for (int fi = 0; fi < kFI; ++fi)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) col[fi][r] = acc[fi][TJ][r];
+}
+
+template <typename T, bool KT>
+__global__ __launch_bounds__(kGemmThreads, 1) void qkv_pack_kernel(GemmArgs g, PackArgs p, RopeSlots tab) {
+    // One 128 KB LDS array: the GEMM's stages, then the epilogue's staging
+    // (4 waves x 16 KB: 64 token rows of 256 bytes) and the tile's parameters
+    // at 64 KB. (A workgroup with more than 128 KB of LDS ran the same GEMM
+    // 20 % slower on MI355X.)
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+    static_assert(kWF == kHead && 4 * 64 * 256 + 2 * 2 * kHead * 4 <= kStages * kStageBytes, "staging layout");
+    TileOf tile;
+    if (!tile.init(g)) return;
+    const int64_t t0 = tile.t0, n0 = tile.n0;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wf = wave & 1, wt = wave >> 1;
+    const int fr = lane & 31, h = lane >> 5;
+    const int hg = (int)((n0 + wf * kWF) / kHead);
+    const int which = hg / p.heads;          // 0 q, 1 k, 2 v (the block's two heads share it)
+    const int z = hg - which * p.heads;
+    const float* __restrict__ bias = which == 0 ? p.bias_q : which == 1 ? p.bias_k : p.bias_v;
+    const float* __restrict__ gamma = which == 0 ? p.gamma_q : which == 1 ? p.gamma_k : nullptr;
+
+    // the tile's bias and gamma * sqrt(D) (one value of each per thread) are
+    // requested before the GEMM and land in LDS after it
+    static_assert(kGemmThreads == 2 * kHead, "one parameter per thread and head");
+    const int ph_ = threadIdx.x / kHead, pd_ = threadIdx.x % kHead;
+    const int pz_ = (int)((n0 + ph_ * kWF) / kHead) - which * p.heads;
+    const float pbias = bias != nullptr ? bias[pz_ * kHead + pd_] : 0.0f;
+    const float pgam = gamma != nullptr ? gamma[pz_ * kHead + pd_] : 0.0f;
+    f32x16 acc[kFI][kTJ];
+    zero_acc(acc);
+    if (t0 < g.rows) gemm_mainloop<T>(g, t0, n0, lds, acc);   // block-uniform (ends with a barrier)
+    float* prm = reinterpret_cast<float*>(lds + 4 * 64 * 256);   // [head][bias, gamma*sqrt(D)][128]
+    prm[(ph_ * 2 + 0) * kHead + pd_] = pbias;
+    prm[(ph_ * 2 + 1) * kHead + pd_] = pgam * p.rms_scale;
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+
+    const bool rope = p.use_rope && which < 2 && g.rows > 0;
+    const int64_t extent = which == 0 ? p.mp : p.lp;
+    T* __restrict__ out = static_cast<T*>(which == 0 ? p.qh : which == 1 ? p.k_out : p.vh);
+    const bool trans = KT && which == 1;
+    uint8_t* region = lds + wave * (64 * 256);
+    const float* pb = prm + (wf * 2 + 0) * kHead;
+    const float* pg = prm + (wf * 2 + 1) * kHead;
+
+#pragma unroll 1
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll 1
+        for (int jj = 0; jj < 2; ++jj) {
+            const int tj = half * 2 + jj;
+            // this token tile's accumulators (static register indices per case)
+            float col[kFI][16];
+            switch (tj) {
+                case 0: copy_col<0>(acc, col); break;
+                case 1: copy_col<1>(acc, col); break;
+                case 2: copy_col<2>(acc, col); break;
+                default: copy_col<3>(acc, col); break;
+            }
+            const int tl = jj * 32 + fr;                      // staged row (token within the half)
+            const int64_t t = t0 + wt * kWT + tj * 32 + fr;
+            const int64_t tc = t < g.rows ? t : g.rows - 1;   // clamped for position reads
+            const bool live = t < g.rows;
+            // feature of col[fi][4q + i]: d = fi*32 + 8q + 4h + i
+            // the token's cos/sin (table path) are requested first and arrive
+            // while the bias and the sum of squares are computed
+            float cs[kFI][4][4];
+            const bool table = rope && p.phases != nullptr;
+            if (table) {
+                const float* row = p.phases + (tc % p.phase_rows) * kHead;
+#pragma unroll
+                for (int fi = 0; fi < kFI; ++fi)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) load_params<4>(row + fi * 32 + q * 8 + h * 4, cs[fi][q]);
+            }
+            if (bias != nullptr) {
+#pragma unroll
+                for (int fi = 0; fi < kFI; ++fi)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 b4 = *reinterpret_cast<const float4*>(pb + fi * 32 + q * 8 + h * 4);
+                        col[fi][q * 4 + 0] = add_rn(col[fi][q * 4 + 0], b4.x);
+                        col[fi][q * 4 + 1] = add_rn(col[fi][q * 4 + 1], b4.y);
+                        col[fi][q * 4 + 2] = add_rn(col[fi][q * 4 + 2], b4.z);
+                        col[fi][q * 4 + 3] = add_rn(col[fi][q * 4 + 3], b4.w);
+                    }
+            }
+            // the head's sum of squares: 64 values here, 64 in lane ^ 32
+            float rn = 1.0f;
+            if (gamma != nullptr) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int fi = 0; fi < kFI; ++fi) ss += sum_sq<16>(col[fi]);
+                ss += __shfl_xor(ss, 32);
+                rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+            }
+            float pos[T2H_MAX_POS_DIM];
+            if (rope && !table) {
+                const PosSource src{p.coords, p.coord_cols, p.grid_res, p.pos_dim};
+                src.get(tc, pos);
+            }
+#pragma unroll
+            for (int fi = 0; fi < kFI; ++fi) {
+                float* v = col[fi];
+                if (gamma != nullptr) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 g4 = *reinterpret_cast<const float4*>(pg + fi * 32 + q * 8 + h * 4);
+                        v[q * 4 + 0] = (v[q * 4 + 0] * rn) * g4.x;
+                        v[q * 4 + 1] = (v[q * 4 + 1] * rn) * g4.y;
+                        v[q * 4 + 2] = (v[q * 4 + 2] * rn) * g4.z;
+                        v[q * 4 + 3] = (v[q * 4 + 3] * rn) * g4.w;
+                    }
+                }
+                if (rope) {
+                    if (table) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            rotate_pair(v[q * 4 + 0], v[q * 4 + 1], cs[fi][q][0], cs[fi][q][1]);
+                            rotate_pair(v[q * 4 + 2], v[q * 4 + 3], cs[fi][q][2], cs[fi][q][3]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j) {
+                                const int sl = (fi * 32 + q * 8 + h * 4) / 2 + j;
+                                float c, sn;
+                                slot_phase(pos, tab.axis[sl], tab.freq[sl], c, sn);
+                                rotate_pair(v[q * 4 + 2 * j], v[q * 4 + 2 * j + 1], c, sn);
+                            }
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float x = which == 0 ? mul_rn(v[r], p.q_scale) : v[r];
+                    v[r] = live ? x : 0.0f;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = fi * 4 + q;                  // 16-byte chunk of the 256-byte token row
+                    u32x2 w;
+                    w.x = Word<T>::pack(&v[q * 4]);
+                    w.y = Word<T>::pack(&v[q * 4 + 2]);
+                    *reinterpret_cast<u32x2*>(region + tl * 256 + ((c ^ stage_swz(tl)) * 16) + h * 8) = w;
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);      // the wave's LDS writes are done (its region is private)
+        const int64_t tw = t0 + wt * kWT + half * 64;   // first token of the staged rows
+        if (!trans) {
+            // token rows: 16 lanes per 256-byte row, 4 rows per instruction
+#pragma unroll 4
+            for (int it = 0; it < 64 / 4; ++it) {
+                const int row = it * 4 + (lane >> 4);
+                const int c = lane & 15;
+                const u32x4 w = *reinterpret_cast<const u32x4*>(region + row * 256 + ((c ^ stage_swz(row)) * 16));
+                const int64_t t = tw + row;
+                if (t < extent) *reinterpret_cast<u32x4*>(out + ((int64_t)z * extent + t) * kHead + c * 8) = w;
+            }
+        } else {
+            // feature rows of the transposed k: lane (d, g) gathers feature d
+            // of tokens 8g .. 8g + 7 (eight 2-byte reads, one per token row)
+#pragma unroll 2
+            for (int it = 0; it < kHead / 8; ++it) {
+                const int d = it * 8 + (lane >> 3);
+                const int gg = lane & 7;
+                const int off = (d & 7) * 2;
+                uint32_t wv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r0 = gg * 8 + 2 * j, r1 = r0 + 1;
+                    const uint32_t lo = *reinterpret_cast<const uint16_t*>(
+                        region + r0 * 256 + (((d >> 3) ^ stage_swz(r0)) * 16) + off);
+                    const uint32_t hi = *reinterpret_cast<const uint16_t*>(
+                        region + r1 * 256 + (((d >> 3) ^ stage_swz(r1)) * 16) + off);
+                    wv[j] = lo | (hi << 16);
+                }
+                const int64_t t = tw + gg * 8;
+                if (t < extent) {
+                    u32x4 w;
+                    w.x = wv[0];
+                    w.y = wv[1];
+                    w.z = wv[2];
+                    w.w = wv[3];
+                    *reinterpret_cast<u32x4*>(out + ((int64_t)z * kHead + d) * p.lp + t) = w;
+                }
+            }
+        }
+        // the next half overwrites the staged rows: every lane's reads are done
+        __builtin_amdgcn_s_waitcnt(0xC07F);
     }
 }
 
@@ -321,6 +622,14 @@ hipError_t gemm_typed(const GemmArgs& a, hipStream_t s) {
     return gemm_act<T, T>(a, s);
 }
 
+template <typename T>
+hipError_t qkv_typed(const GemmArgs& g, const PackArgs& p, const RopeSlots& tab, hipStream_t s) {
+    const dim3 grid = grid_1d(g.nblocks), blk(kGemmThreads);
+    if (p.k_transposed) hipLaunchKernelGGL((qkv_pack_kernel<T, true>), grid, blk, 0, s, g, p, tab);
+    else hipLaunchKernelGGL((qkv_pack_kernel<T, false>), grid, blk, 0, s, g, p, tab);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 int32_t gemm_feature_tile() { return kBF; }
@@ -332,6 +641,20 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.nblocks == 0) return hipSuccess;
     if (a.dtype == T2H_F16) return gemm_typed<_Float16>(a, s);
     return gemm_typed<__bf16>(a, s);
+}
+
+int32_t gemm_head_dim() { return kHead; }
+
+hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, hipStream_t s) {
+    // token tiles cover the pad rows of the outputs too (they are written as 0)
+    int64_t span = g.rows;
+    if (p.mp > span) span = p.mp;
+    if (p.lp > span) span = p.lp;
+    g.ftiles = g.n / kBF;
+    g.nblocks = ((span + kBT - 1) / kBT) * g.ftiles;
+    if (g.nblocks == 0) return hipSuccess;
+    if (g.dtype == T2H_F16) return qkv_typed<_Float16>(g, p, tab, s);
+    return qkv_typed<__bf16>(g, p, tab, s);
 }
 
 }  // namespace t2h

@@ -195,6 +195,8 @@ hipError_t launch_pack(const PackArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_gemm(GemmArgs a, hipStream_t s);
 int32_t gemm_feature_tile();   // output features per block (out_features must be a multiple)
 int32_t gemm_k_step();         // k per stage (in_features must be a multiple)
+int32_t gemm_head_dim();       // head_dim of the fused qkv GEMM + pack
+hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, hipStream_t s);
 // t2h_sampler.hip
 hipError_t launch_euler(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
 // t2h_eltwise.hip

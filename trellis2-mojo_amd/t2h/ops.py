@@ -305,6 +305,64 @@ def attn_pack(q=None, k=None, v=None, mp: int = 0, lp: int = 0, bias_q=None, bia
     return qh, ko, vh
 
 
+def qkv_linear_pack(x, weight, heads: int, bias=None, gamma_q=None, gamma_k=None, mp: int = 0, lp: int = 0,
+                    freqs=None, pos_dim: int = 3, phases=None, coords=None, grid_res: int = 0, use_rope: bool = True,
+                    k_transposed: bool = True):
+    """The qkv linear fused with the attention epilogue and the head-major
+    pack: x [rows, K] (float16/bfloat16, rows may be strided), weight
+    [3*H*D, K] of x's dtype, bias [3*H*D] float32 (or None), gammas [H, D]
+    float32 -> (qh [H, mp, D] scaled by 1/sqrt(D), k [H, D, lp] (k_transposed)
+    or [H, lp, D], vh [H, lp, D]); pads zero; mp/lp 0 = rows. D = 128."""
+    _dev(x, "qkv_linear_pack")
+    _dev(weight, "qkv_linear_pack")
+    dt = _dtype(x, "qkv_linear_pack")
+    if weight.dtype != x.dtype or weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("qkv_linear_pack: weight must be a contiguous [3*H*D, K] tensor of x's dtype")
+    n, k = weight.shape
+    if n % (3 * heads) != 0:
+        raise ValueError("qkv_linear_pack: weight rows must be 3 * heads * head_dim")
+    d = n // (3 * heads)
+    if x.dim() != 2 or x.shape[1] != k or x.stride(1) != 1:
+        raise ValueError("qkv_linear_pack: x must be [rows, K] with unit column stride")
+    rows, ldx = x.shape[0], (x.stride(0) if x.shape[0] > 1 else k)
+    bq = bk = bv = None
+    if bias is not None:
+        _dev(bias, "qkv_linear_pack")
+        if bias.dtype != torch.float32 or bias.numel() != n or not bias.is_contiguous():
+            raise ValueError("qkv_linear_pack: bias must be a contiguous float32 [3*H*D] tensor")
+        bq, bk, bv = bias.reshape(3, heads * d).unbind(0)
+    for g in (gamma_q, gamma_k):
+        if g is not None:
+            _dev(g, "qkv_linear_pack")
+            if g.dtype != torch.float32 or g.numel() != heads * d or not g.is_contiguous():
+                raise ValueError("qkv_linear_pack: gammas must be contiguous float32 [H, D]")
+    mp = mp or rows
+    lp = lp or rows
+    mk = lambda shape: torch.empty(shape, dtype=x.dtype, device=x.device)
+    qh = mk((heads, mp, d))
+    ko = mk((heads, d, lp)) if k_transposed else mk((heads, lp, d))
+    vh = mk((heads, lp, d))
+    hold, fp, fd = _host_freqs(freqs if freqs is not None else [])
+    ph_rows = 0
+    if phases is not None:
+        _dev(phases, "qkv_linear_pack")
+        if phases.dtype != torch.float32 or not phases.is_contiguous() or phases.shape[-2:] != (d // 2, 2):
+            raise ValueError("apply_rotary_embedding: phases shape mismatch")
+        ph_rows = phases.numel() // d
+    cc = 0
+    if coords is not None:
+        _dev(coords, "qkv_linear_pack")
+        if coords.dtype != torch.int32 or not coords.is_contiguous() or coords.shape[0] != rows:
+            raise ValueError("qkv_linear_pack: coords must be contiguous int32 [rows, 1+pos_dim]")
+        cc = coords.shape[1]
+    p = lambda t: t.data_ptr() if t is not None else None
+    call("t2h_qkv_linear_pack", x.data_ptr(), ldx, weight.data_ptr(), rows, k, heads, d, dt, p(bq), p(bk), p(bv),
+         p(gamma_q), p(gamma_k), int(bool(use_rope)), fp, fd, int(pos_dim), p(phases), ph_rows, p(coords), cc,
+         int(grid_res), qh.data_ptr(), mp, ko.data_ptr(), vh.data_ptr(), lp, int(bool(k_transposed)), _stream())
+    del hold
+    return qh, ko, vh
+
+
 def rope_phases(rows: int, head_dim: int, freqs, pos_dim: int = 3, positions=None, coords=None, grid_res: int = 0,
                 device=None) -> torch.Tensor:
     """Phase table [rows, head_dim/2, 2] (cos, sin) f32."""
