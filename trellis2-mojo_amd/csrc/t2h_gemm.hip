@@ -60,6 +60,9 @@ template <> struct Mfma<__bf16> {
 #ifndef T2H_GEMM_BK
 #define T2H_GEMM_BK 64
 #endif
+#ifndef T2H_GEMM_STAGES
+#define T2H_GEMM_STAGES 2
+#endif
 #ifndef T2H_GEMM_OCC
 #define T2H_GEMM_OCC 1
 #endif
@@ -70,7 +73,7 @@ constexpr int kBT = T2H_GEMM_BT;          // tokens per block
 constexpr int kBK = T2H_GEMM_BK;          // k per stage
 constexpr int kCpr = kBK / 8;             // 16-byte chunks per tile row
 constexpr int kSub = kBK / 16;            // MFMA k substeps per stage
-constexpr int kStages = 2;               // LDS stages (double buffer)
+constexpr int kStages = T2H_GEMM_STAGES;  // LDS stages; loads run up to kStages stages ahead
 constexpr int kWF = kBF / 2;              // features per wave
 constexpr int kWT = kBT / 2;              // tokens per wave
 constexpr int kFI = kWF / 32;             // MFMA tiles along features
@@ -83,7 +86,8 @@ constexpr int kLoadsA = kChunksA / 64 / 4;   // 64-lane loads per wave per stage
 constexpr int kLoadsB = kChunksB / 64 / 4;
 constexpr int kLoads = kLoadsA + kLoadsB;
 static_assert(kCpr == 4 || kCpr == 8, "k step of 32 or 64");
-static_assert(kLoads < 64, "vmcnt range");
+static_assert(kStages >= 2 && kStages * kStageBytes <= 128 * 1024, "stages fit 128 KB of LDS");
+static_assert((kStages - 1) * kLoads < 64, "vmcnt range");
 
 // Tile u of nb, dealt so that XCD x (blocks b with b % 8 == x) takes the
 // contiguous range of tiles [x*q + min(x, r), ...): a bijection of [0, nb).
@@ -146,17 +150,19 @@ struct StageCtx {
     int fa, fb, slot, wave;
 };
 
-// One k step (stage ks, in LDS buffer ks & 1): kSub substeps of kFI x kTJ
-// MFMAs. Substep s + 1's fragments are read while substep s's MFMAs run (the
-// scheduling groups interleave 1 MFMA : 1 LDS read, then the remaining
-// MFMAs). In the last substep, when NEXT: wait for stage ks + 1's loads, the
-// barrier that publishes them (after it every wave has finished reading
-// stage ks), stage ks + 2's loads into stage ks's buffer when ISSUE, and
-// stage ks + 1's first fragments interleaved with the last MFMAs.
-template <typename T, bool NEXT, bool ISSUE>
+// One k step (stage ks, in LDS buffer ks % kStages): kSub substeps of
+// kFI x kTJ MFMAs. Substep s + 1's fragments are read while substep s's
+// MFMAs run (the scheduling groups interleave 1 MFMA : 1 LDS read, then the
+// remaining MFMAs). In the last substep, when NEXT: wait for stage ks + 1's
+// loads (PEND later stages may still be in flight), the barrier that
+// publishes them (after it every wave has finished reading stage ks), stage
+// ks + kStages's loads into stage ks's buffer when ISSUE, and stage ks + 1's
+// first fragments interleaved with the last MFMAs.
+template <typename T, bool NEXT, bool ISSUE, int PEND>
 __device__ __forceinline__ void stage_body(f32x16 (&acc)[kFI][kTJ], typename Mfma<T>::v8 (&af)[2][kFI],
                                            typename Mfma<T>::v8 (&bf)[2][kTJ], const StageCtx& cx, int ks) {
-    const uint8_t* st = cx.lds + (ks & 1) * kStageBytes;
+    const int buf = ks % kStages;
+    const uint8_t* st = cx.lds + buf * kStageBytes;
 #pragma unroll
     for (int s = 0; s < kSub; ++s) {
         const int c = s & 1, n = c ^ 1;
@@ -164,11 +170,11 @@ __device__ __forceinline__ void stage_body(f32x16 (&acc)[kFI][kTJ], typename Mfm
         if (!last) {
             read_frags<T>(af[n], bf[n], st, cx.fa, cx.fb, cx.slot ^ (32 * (s + 1)));
         } else if (NEXT) {
-            wait_vm<0>();
+            wait_vm<PEND * kLoads>();
             __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0)
             __builtin_amdgcn_s_barrier();
-            if (ISSUE) issue_stage(cx.wbase, cx.xbase, cx.src, ks + 2, cx.lds + (ks & 1) * kStageBytes, cx.wave);
-            read_frags<T>(af[n], bf[n], cx.lds + ((ks + 1) & 1) * kStageBytes, cx.fa, cx.fb, cx.slot);
+            if (ISSUE) issue_stage(cx.wbase, cx.xbase, cx.src, ks + kStages, cx.lds + buf * kStageBytes, cx.wave);
+            read_frags<T>(af[n], bf[n], cx.lds + ((ks + 1) % kStages) * kStageBytes, cx.fa, cx.fb, cx.slot);
         }
 #pragma unroll
         for (int fi = 0; fi < kFI; ++fi)
@@ -183,6 +189,16 @@ __device__ __forceinline__ void stage_body(f32x16 (&acc)[kFI][kTJ], typename Mfm
             __builtin_amdgcn_sched_group_barrier(0x008, kFI * kTJ - (kFI + kTJ), 0);
         }
         __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// wait_vm<n * kLoads> for a small runtime stage count n
+__device__ __forceinline__ void wait_stages(int n) {
+    switch (n) {
+        case 0: wait_vm<0>(); break;
+        case 1: wait_vm<kLoads>(); break;
+        case 2: wait_vm<(kStages > 2 ? 2 : 1) * kLoads>(); break;
+        default: wait_vm<(kStages > 3 ? 3 : 1) * kLoads>(); break;
     }
 }
 
@@ -252,32 +268,35 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& a, int64_t t0, int
     const int fb = kChunksA * 16 + (wt * kWT + fr) * kRowBytes;
 
     const int ksteps = a.k / kBK;
-    // Two LDS stages. Stage ks + 1's loads are issued while stage ks is
-    // computed; the barrier that publishes them sits in stage ks's last
-    // substep, so stage ks + 1's first fragments are read while stage ks's
-    // last MFMAs run. Right after that barrier every wave has finished
-    // reading stage ks (its reads completed before the barrier), so stage
-    // ks + 2's loads go into stage ks's buffer.
-    issue_stage(wbase, xbase, src, 0, lds, wave);
-    if (ksteps > 1) {
-        issue_stage(wbase, xbase, src, 1, lds + kStageBytes, wave);
-        wait_vm<kLoads>();
-    } else {
-        wait_vm<0>();
-    }
+    // kStages LDS stages. The prologue issues the first kStages steps. At the
+    // barrier in stage ks's last substep (stage ks + 1 has landed; up to
+    // kStages - 2 later stages are in flight), every wave has finished reading
+    // stage ks, so stage ks + kStages's loads go into stage ks's buffer, and
+    // stage ks + 1's first fragments are read while stage ks's last MFMAs run.
+    const int pro = ksteps < kStages ? ksteps : kStages;
+#pragma unroll
+    for (int st = 0; st < kStages; ++st)
+        if (st < pro) issue_stage(wbase, xbase, src, st, lds + st * kStageBytes, wave);
+    wait_stages(pro - 1);
     __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
 
     V8 af[2][kFI], bf[2][kTJ];
     read_frags<T>(af[0], bf[0], lds, fa, fb, slot);
     __builtin_amdgcn_sched_barrier(0);
-    // branch-free steady state, then the last two stages (no further loads;
-    // no next stage)
+    // branch-free steady state, then the tail (no further loads; fewer
+    // stages in flight), then the last stage (no next stage)
     const StageCtx cx{wbase, xbase, src, lds, fa, fb, slot, wave};
     int ks = 0;
-    for (; ks + 2 < ksteps; ++ks) stage_body<T, true, true>(acc, af, bf, cx, ks);
-    if (ks + 1 < ksteps) stage_body<T, true, false>(acc, af, bf, cx, ks++);
-    stage_body<T, false, false>(acc, af, bf, cx, ks);
+    for (; ks + kStages < ksteps; ++ks) stage_body<T, true, true, kStages - 2>(acc, af, bf, cx, ks);
+    // the last r = ksteps - ks <= kStages stages, straight-line: stage i of
+    // the tail has r - 2 - i stages in flight after its next one
+    static_assert(kStages <= 4, "tail cases");
+    const int r = ksteps - ks;
+    if (kStages > 3 && r >= 4) stage_body<T, true, false, (kStages > 3 ? 2 : 0)>(acc, af, bf, cx, ks++);
+    if (kStages > 2 && r >= 3) stage_body<T, true, false, (kStages > 2 ? 1 : 0)>(acc, af, bf, cx, ks++);
+    if (r >= 2) stage_body<T, true, false, 0>(acc, af, bf, cx, ks++);
+    stage_body<T, false, false, 0>(acc, af, bf, cx, ks);
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();                // every wave is done reading the stages
 }
