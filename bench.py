@@ -30,6 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "trellis2-mojo_amd"))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16/bf16 matrix peak
 METRIC = "fused-layer HBM GB/s (% of MI355X peak) and tokens/s at width 1536, 1 GPU"
 
 
@@ -116,7 +117,35 @@ class Chain:
             return lambda: self.torch.mul(self.u, 1.0, out=self.gout)
         if name == "chain":
             return self.step
+        if name in self.GEMM_OPS:
+            g = self.gemm_state()
+            if name == "linear_qkv":
+                return lambda: o.linear(self.x, g["wqkv"], out=g["out"][:, :3 * self.C])
+            if name == "linear_fc1_gelu":
+                return lambda: o.linear(self.x, g["w1"], bias=self.bias, act=o.ACT_GELU_TANH, out=g["out"])
+            return lambda: o.qkv_linear_pack(self.x, g["wqkv"], self.H, bias=self.bias[:3 * self.C], gamma_q=self.gq,
+                                             gamma_k=self.gk, mp=g["mp"], lp=g["mp"], freqs=self.freqs,
+                                             phases=g["phases"], k_transposed=True)
         raise KeyError(name)
+
+    # the GEMM rows (f16 operands on the matrix cores): flops per launch
+    GEMM_OPS = ("linear_qkv", "linear_fc1_gelu", "qkv_linear_pack")
+
+    def gemm_flops(self, name):
+        n = self.F if name == "linear_fc1_gelu" else 3 * self.C
+        return 2.0 * self.T * n * self.C
+
+    def gemm_state(self):
+        if getattr(self, "_gemm", None) is None:
+            torch, o = self.torch, self.ops
+            g = torch.Generator(device=self.x.device).manual_seed(9)
+            rw = lambda n: (torch.randn((n, self.C), generator=g, device=self.x.device) * 0.02).to(self.x.dtype)
+            self._gemm = {"wqkv": rw(3 * self.C), "w1": rw(self.F),
+                          "out": torch.empty((self.T, self.F), dtype=self.x.dtype, device=self.x.device),
+                          "mp": (self.T + 63) // 64 * 64,
+                          "phases": o.rope_phases(self.T, self.D, self.freqs, coords=self.coords,
+                                                  device=self.x.device)}
+        return self._gemm
 
     ORDER = ["timestep", "ln_modulate", "qk_rmsnorm_rope", "gelu_tanh_bias", "gate_residual"]
 
@@ -307,6 +336,47 @@ def next_rows(torch, dev, chain, reps):
                                                                    guidance_strength=3.0, guidance_rescale=0.5,
                                                                    seg_offsets=[0, T], workspace=ws), 8 * n)
     del lat, ws
+    # N2's GEMM half on the matrix cores (f16 operands, f32 sums), config-5
+    # tokens: the qkv linear alone, the MLP's first linear with GELU-tanh in
+    # its store, and the qkv linear fused with the attention epilogue and the
+    # head-major pack (RoPE from the phase table, built once per forward as
+    # the reference does); hipBLASLt (torch.matmul) + the separate pack beside
+    # them.
+    def rec_f(name, fn, flops):
+        fn()
+        ms = time_region(torch, fn, reps) / reps
+        tf = flops / ms / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "flops": flops, "tflops": round(tf, 1),
+                     "pct_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS * 100, 2)}
+        log(f"  {name:<26s} {ms*1e3:8.1f} us  {tf:8.1f} TFLOP/s ({tf/MFMA_F16_PEAK_TFLOPS*100:5.1f}% of f16 MFMA)")
+
+    g = torch.Generator(device=dev).manual_seed(9)
+    wqkv = (torch.randn((3 * C, C), generator=g, device=dev) * 0.02).to(torch.float16)
+    w1 = (torch.randn((chain.F, C), generator=g, device=dev) * 0.02).to(torch.float16)
+    xg = chain.x
+    out = torch.empty((T, chain.F), dtype=torch.float16, device=dev)
+    fq = 2.0 * T * 3 * C * C
+    rec_f("linear_qkv", lambda: ops.linear(xg, wqkv, out=out[:, :3 * C]), fq)
+    rec_f("linear_fc1_gelu", lambda: ops.linear(xg, w1, bias=chain.bias, act=ops.ACT_GELU_TANH, out=out),
+          2.0 * T * chain.F * C)
+    ph = ops.rope_phases(T, D, chain.freqs, coords=chain.coords, device=dev)
+    bq = chain.bias[:3 * C]
+    for kt in (True, False):
+        rec_f(f"qkv_linear_pack_k{'t' if kt else 'rows'}",
+              lambda kt=kt: ops.qkv_linear_pack(xg, wqkv, H, bias=bq, gamma_q=chain.gq, gamma_k=chain.gk, mp=mp,
+                                                lp=mp, freqs=chain.freqs, phases=ph, k_transposed=kt), fq)
+    qkv = out[:, :3 * C].contiguous()
+    q3 = qkv.reshape(T, 3, H, D)
+    b3 = bq.reshape(3, H * D)
+
+    def hipblaslt_then_pack():
+        torch.matmul(xg, wqkv.t(), out=qkv)
+        ops.attn_pack(q3[:, 0], q3[:, 1], q3[:, 2], mp=mp, lp=mp, bias_q=b3[0], bias_k=b3[1], bias_v=b3[2],
+                      gamma_q=chain.gq, gamma_k=chain.gk, freqs=chain.freqs, phases=ph, k_transposed=True)
+
+    rec_f("hipblaslt_qkv", lambda: torch.matmul(xg, wqkv.t(), out=qkv), fq)
+    rec_f("hipblaslt_qkv_then_pack_kt", hipblaslt_then_pack, fq)
+    del wqkv, w1, out, ph, qkv, q3
     return res
 
 
@@ -332,6 +402,10 @@ def main():
         for _ in range(args.warmup):
             fn()
         ms = time_region(torch, fn, args.steps)
+        if args.op in chain.GEMM_OPS:
+            tf = chain.gemm_flops(args.op) / (ms / args.steps) / 1e9
+            log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {tf:.1f} TFLOP/s")
+            return
         nb = chain.chain_bytes if args.op == "chain" else chain.bytes[args.op]
         log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {nb/(ms/args.steps)/1e6:.1f} GB/s")
         return

@@ -90,6 +90,11 @@ def test_strided_rows_and_leading_dims(dev):
     assert torch.equal(got, ref)
     got3 = ops.linear(to_dev(a, dev, torch.float16).reshape(4, 50, k), wd, out_dtype=torch.float32)
     assert got3.shape == (4, 50, n) and torch.equal(got3.reshape(m, n), ref)
+    # output rows of a wider buffer (ldo > n), 16-bit staged store
+    wide_out = torch.full((m, n + 128), 7.0, dtype=torch.float16, device=dev)
+    ops.linear(to_dev(a, dev, torch.float16), wd, out=wide_out[:, 64:64 + n])
+    assert torch.equal(wide_out[:, 64:64 + n], ops.linear(to_dev(a, dev, torch.float16), wd))
+    assert bool((wide_out[:, :64] == 7).all()) and bool((wide_out[:, 64 + n:] == 7).all())
 
 
 def test_zero_rows_and_shape_errors(dev):

@@ -209,16 +209,37 @@ __device__ __forceinline__ float epi_f(float acc, float b) {
     else return act_f<ACT>(v);
 }
 
-// Block tile of a launch: token tile t0 and feature tile n0 of block b.
+#ifndef T2H_GEMM_TG
+#define T2H_GEMM_TG 4
+#endif
+constexpr int kTokGroup = T2H_GEMM_TG;   // token tiles per group (0: token-tile-major order)
+
+// Block tile of a launch: token tile t0 and feature tile n0 of block b. The
+// XCD deal gives each XCD a contiguous range of tile numbers; within groups
+// of kTokGroup token tiles the numbers walk feature tile by feature tile, so
+// the blocks resident on an XCD at once share a few weight slabs and a few
+// token slabs in its L2 (a bijection of [0, nblocks)).
 struct TileOf {
     int64_t t0, n0;
     __device__ __forceinline__ bool init(const GemmArgs& a) {
         const int64_t b = block_linear();
         if (b >= a.nblocks) return false;
         const int64_t u = xcd_tile(b, a.nblocks);
-        const int64_t tt = u / a.ftiles;
+        int64_t tt, ft;
+        if constexpr (kTokGroup > 0) {
+            const int64_t ntok = a.nblocks / a.ftiles;
+            const int64_t gsz = (int64_t)kTokGroup * a.ftiles;
+            const int64_t g = u / gsz, off = u - g * gsz;
+            const int64_t rem = ntok - g * kTokGroup;
+            const int64_t tg = rem < kTokGroup ? rem : kTokGroup;
+            tt = g * kTokGroup + off % tg;
+            ft = off / tg;
+        } else {
+            tt = u / a.ftiles;
+            ft = u - tt * a.ftiles;
+        }
         t0 = tt * kBT;
-        n0 = (u - tt * a.ftiles) * kBF;
+        n0 = ft * kBF;
         return true;
     }
 };
@@ -412,7 +433,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
 // feature gathered from 8 rows. Tiles past the last token row skip the GEMM
 // and write the pads.
 constexpr int kHead = 128;
-static_assert(kTJ == 4, "copy_col cases");
+static_assert(kTJ == 2 || kTJ == 4, "copy_col cases");
 
 // Slot of a 16-byte chunk in a staged 256-byte token row: chunk c of row r
 // at c ^ stage_swz(r). Over 32 consecutive rows (one row-major write) every
@@ -429,13 +450,14 @@ __device__ __forceinline__ void copy_col(const f32x16 (&acc)[kFI][kTJ], float (&
 }
 
 template <typename T, bool KT>
-__global__ __launch_bounds__(kGemmThreads, 1) void qkv_pack_kernel(GemmArgs g, PackArgs p, RopeSlots tab) {
-    // One 128 KB LDS array: the GEMM's stages, then the epilogue's staging
-    // (4 waves x 16 KB: 64 token rows of 256 bytes) and the tile's parameters
-    // at 64 KB. (A workgroup with more than 128 KB of LDS ran the same GEMM
-    // 20 % slower on MI355X.)
+__global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(GemmArgs g, PackArgs p, RopeSlots tab) {
+    // One LDS array: the GEMM's stages, then the epilogue's staging (4 waves
+    // x 16 KB: 64 token rows of 256 bytes) and the tile's parameters at 64 KB.
+    // (A separate parameter array that took the kernel past 128 KB of LDS
+    // measured 20 % slower on MI355X.)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
-    static_assert(kWF == kHead && 4 * 64 * 256 + 2 * 2 * kHead * 4 <= kStages * kStageBytes, "staging layout");
+    static_assert(kWF == kHead && kWT % 64 == 0 && 4 * 64 * 256 + 2 * 2 * kHead * 4 <= kStages * kStageBytes,
+                  "staging layout");
     TileOf tile;
     if (!tile.init(g)) return;
     const int64_t t0 = tile.t0, n0 = tile.n0;
@@ -475,7 +497,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qkv_pack_kernel(GemmArgs g, P
     const float* pg = prm + (wf * 2 + 1) * kHead;
 
 #pragma unroll 1
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < kTJ / 2; ++half) {
 #pragma unroll 1
         for (int jj = 0; jj < 2; ++jj) {
             const int tj = half * 2 + jj;
@@ -484,8 +506,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qkv_pack_kernel(GemmArgs g, P
             switch (tj) {
                 case 0: copy_col<0>(acc, col); break;
                 case 1: copy_col<1>(acc, col); break;
-                case 2: copy_col<2>(acc, col); break;
-                default: copy_col<3>(acc, col); break;
+                case 2: copy_col<(kTJ > 2 ? 2 : 0)>(acc, col); break;
+                default: copy_col<(kTJ > 2 ? 3 : 1)>(acc, col); break;
             }
             const int tl = jj * 32 + fr;                      // staged row (token within the half)
             const int64_t t = t0 + wt * kWT + tj * 32 + fr;

@@ -418,10 +418,16 @@ def linear(x, weight, bias=None, act: int = ACT_NONE, out_dtype=None, out=None) 
     od = x.dtype if out_dtype is None else out_dtype
     if out is None:
         out = torch.empty((*x.shape[:-1], n), dtype=od, device=x.device)
-    elif out.dtype != od or out.shape != (*x.shape[:-1], n) or not out.is_contiguous():
-        raise ValueError("linear: out must be a contiguous [..., N] tensor of out_dtype")
+    elif out.dtype != od or out.shape != (*x.shape[:-1], n):
+        raise ValueError("linear: out must be a [..., N] tensor of out_dtype")
+    if out.is_contiguous():
+        ldo = n
+    elif out.dim() == 2 and out.stride(1) == 1 and out.stride(0) >= n:
+        ldo = out.stride(0)   # rows of a wider buffer
+    else:
+        raise ValueError("linear: out must be contiguous, or [rows, N] with unit column stride")
     call("t2h_linear", x2.data_ptr(), ldx, weight.data_ptr(), bias.data_ptr() if bias is not None else None,
-         out.data_ptr(), n, rows, k, n, dt, _dtype(out, "linear"), int(act), _stream())
+         out.data_ptr(), ldo, rows, k, n, dt, _dtype(out, "linear"), int(act), _stream())
     return out
 
 
