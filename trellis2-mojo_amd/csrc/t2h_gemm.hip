@@ -63,6 +63,9 @@ template <> struct Mfma<__bf16> {
 #ifndef T2H_GEMM_STAGES
 #define T2H_GEMM_STAGES 2
 #endif
+#ifndef T2H_GEMM_DMAI
+#define T2H_GEMM_DMAI 1
+#endif
 #ifndef T2H_GEMM_OCC
 #define T2H_GEMM_OCC 1
 #endif
@@ -180,7 +183,24 @@ __device__ __forceinline__ void stage_body(f32x16 (&acc)[kFI][kTJ], typename Mfm
         for (int fi = 0; fi < kFI; ++fi)
 #pragma unroll
             for (int tj = 0; tj < kTJ; ++tj) acc[fi][tj] = Mfma<T>::run(af[c][fi], bf[c][tj], acc[fi][tj]);
-        if (!last || NEXT) {
+        if (last && NEXT && ISSUE && T2H_GEMM_DMAI) {
+            // the next stage's loads (kLoads per wave) go out between this
+            // substep's first MFMAs, its first fragments between the rest
+            // (the LDS reads stay behind the loads' m0 writes)
+            constexpr int kG = kFI + kTJ;
+            static_assert(kLoads % kG == 0 && kFI * kTJ >= 2 * kG, "groups");
+#pragma unroll
+            for (int g = 0; g < kG; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x010, kLoads / kG, 0);    // VMEM (to LDS)
+            }
+#pragma unroll
+            for (int g = 0; g < kG; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, kFI * kTJ - 2 * kG, 0);
+        } else if (!last || NEXT) {
 #pragma unroll
             for (int g = 0; g < kFI + kTJ; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
