@@ -123,15 +123,20 @@ class Chain:
                 return lambda: o.linear(self.x, g["wqkv"], out=g["out"][:, :3 * self.C])
             if name == "linear_fc1_gelu":
                 return lambda: o.linear(self.x, g["w1"], bias=self.bias, act=o.ACT_GELU_TANH, out=g["out"])
+            if name == "linear_fc2_gate_residual":
+                return lambda: o.linear_gate_residual(self.u, g["w2"], self.x, bias=self.bias[:self.C],
+                                                      gate=self.gate, offsets=self.offsets, out=self.res)
             return lambda: o.qkv_linear_pack(self.x, g["wqkv"], self.H, bias=self.bias[:3 * self.C], gamma_q=self.gq,
                                              gamma_k=self.gk, mp=g["mp"], lp=g["mp"], freqs=self.freqs,
                                              phases=g["phases"], k_transposed=True)
         raise KeyError(name)
 
     # the GEMM rows (f16 operands on the matrix cores): flops per launch
-    GEMM_OPS = ("linear_qkv", "linear_fc1_gelu", "qkv_linear_pack")
+    GEMM_OPS = ("linear_qkv", "linear_fc1_gelu", "qkv_linear_pack", "linear_fc2_gate_residual")
 
     def gemm_flops(self, name):
+        if name == "linear_fc2_gate_residual":
+            return 2.0 * self.T * self.C * self.F
         n = self.F if name == "linear_fc1_gelu" else 3 * self.C
         return 2.0 * self.T * n * self.C
 
@@ -141,6 +146,8 @@ class Chain:
             g = torch.Generator(device=self.x.device).manual_seed(9)
             rw = lambda n: (torch.randn((n, self.C), generator=g, device=self.x.device) * 0.02).to(self.x.dtype)
             self._gemm = {"wqkv": rw(3 * self.C), "w1": rw(self.F),
+                          "w2": (torch.randn((self.C, self.F), generator=g, device=self.x.device) * 0.02).to(
+                              self.x.dtype),
                           "out": torch.empty((self.T, self.F), dtype=self.x.dtype, device=self.x.device),
                           "mp": (self.T + 63) // 64 * 64,
                           "phases": o.rope_phases(self.T, self.D, self.freqs, coords=self.coords,
@@ -377,6 +384,21 @@ def next_rows(torch, dev, chain, reps):
     rec_f("hipblaslt_qkv", lambda: torch.matmul(xg, wqkv.t(), out=qkv), fq)
     rec_f("hipblaslt_qkv_then_pack_kt", hipblaslt_then_pack, fq)
     del wqkv, w1, out, ph, qkv, q3
+    # the MLP's second linear with the gated residual join in its store
+    # (x += (h + bias) * gate[b]), against hipBLASLt + the separate join
+    w2 = (torch.randn((C, chain.F), generator=g, device=dev) * 0.02).to(torch.float16)
+    hmid = torch.empty((T, C), dtype=torch.float16, device=dev)
+    f2 = 2.0 * T * C * chain.F
+    rec_f("linear_fc2_gate_residual",
+          lambda: ops.linear_gate_residual(chain.u, w2, chain.x, bias=chain.bias[:C], gate=chain.gate,
+                                           offsets=chain.offsets, out=chain.res), f2)
+
+    def hipblaslt_fc2_then_join():
+        torch.matmul(chain.u, w2.t(), out=hmid)
+        ops.gate_residual(chain.x, hmid, gate=chain.gate, bias=chain.bias[:C], offsets=chain.offsets, out=chain.res)
+
+    rec_f("hipblaslt_fc2_then_gate_residual", hipblaslt_fc2_then_join, f2)
+    del w2, hmid
     return res
 
 

@@ -202,6 +202,28 @@ int32_t t2h_attn_pack(const void* q, const void* k, const void* v,
                       int64_t mp, void* k_out, void* vh, int64_t lp,
                       int32_t k_transposed, void* stream);
 
+/* ---- linear fused with the gated residual join ------------------------------
+ * out[t, n] = res[t, n] + fl(fl(sum_k x[t, k] * w[n, k] + bias[n]) * gate[b(t), n])
+ * (gate NULL: res + fl(acc + bias)): the block's residual join in the store
+ * of the GEMM that makes h.
+ * Replaces: the out linear's GpuLinear.enqueue_gemm (attention out-projection,
+ * the MLP's lin2: gpu/linear.mojo:535-560, 776-809) followed by
+ * gate_add_bias_rows (gpu/block.mojo:86-110, sequence 317-397), and the CPU
+ * form x + h.elemwise_batch(gate, MUL) with per-batch gate rows
+ * (sparse/transformer/modulated.mojo:214-226).
+ * x, w, bias, shapes and alignment as t2h_linear; res and out [rows,
+ * out_features] (rows ldo elements apart) in out_dtype (f32 or dtype); out
+ * may alias res. gate rows gate_stride apart (0 = out_features), batch of a
+ * row from offsets [nbatch + 1] or rows_per_batch, as t2h_gate_residual. */
+int32_t t2h_linear_gate_residual(const void* x, int64_t ldx, const void* w,
+                                 const float* bias, const void* res,
+                                 void* out, int64_t ldo, int64_t rows,
+                                 int32_t in_features, int32_t out_features,
+                                 int32_t dtype, int32_t out_dtype,
+                                 const float* gate, int64_t gate_stride,
+                                 const int64_t* offsets, int32_t nbatch,
+                                 int64_t rows_per_batch, void* stream);
+
 /* ---- qkv linear fused with the attention epilogue and head-major pack -----
  * The self-attention chain's qkv GEMM, bias_rms_rope_qkv, pack_q_z and
  * pack_kv_z in one kernel: the GEMM's [rows, 3, H, D] output stays in

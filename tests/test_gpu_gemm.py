@@ -108,3 +108,69 @@ def test_zero_rows_and_shape_errors(dev):
                    torch.zeros((256, 40), dtype=torch.float16, device=dev))
     with pytest.raises(ValueError, match="f16 or bf16"):
         ops.linear(torch.zeros((4, 64), device=dev), torch.zeros((256, 64), device=dev))
+
+
+# ---- linear + gated residual join (t2h_linear_gate_residual) -------------------
+def _int_case(seed, m, n, k, lo=-4, hi=5):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(lo, hi, (m, k)).astype(np.float32)
+    w = rng.integers(lo, hi, (n, k)).astype(np.float32)
+    return rng, a, w
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gate_residual_integer_bit_exact(dev, dtype):
+    """Exact GEMM sums (small integers), per-batch power-of-two gates over two
+    ragged sparse batches, integer bias and residual: every output equals the
+    oracle's gate_residual on the oracle's GEMM bit for bit, written to a
+    fresh tensor and in place over the residual (the block's x += ...)."""
+    m, n, k = 300, 512, 128
+    rng, a, w = _int_case(21, m, n, k, -2, 3)
+    bias = rng.integers(-3, 4, (n,)).astype(np.float32)
+    gate = (2.0 ** rng.integers(-2, 2, (2, n))).astype(np.float32)
+    res = rng.integers(-8, 9, (m, n)).astype(np.float32)
+    offsets = np.array([0, 137, m], np.int64)
+    want = orc.gate_residual(res, orc.linear(a, w), gate, offsets, bias)
+    assert np.abs(want).max() < 256
+    args = dict(bias=to_dev(bias, dev), gate=to_dev(gate, dev), offsets=to_dev(offsets, dev))
+    ad, wd = to_dev(a, dev, dtype), to_dev(w, dev, dtype)
+    rd = to_dev(res, dev, dtype)
+    got = ops.linear_gate_residual(ad, wd, rd, **args)
+    assert np.array_equal(host(got), want)
+    ops.linear_gate_residual(ad, wd, rd, out=rd, **args)
+    assert np.array_equal(host(rd), want)
+    # f32 residual stream
+    r32 = to_dev(res, dev)
+    assert np.array_equal(host(ops.linear_gate_residual(ad, wd, r32, **args)), want)
+
+
+def test_gate_residual_f32_stream_random(dev):
+    """Random f16 operands onto an f32 residual stream (the reference's f32
+    residual), per-batch gates by rows_per_batch: within the GEMM's sum bound
+    times |gate| of the oracle (the rest of the join is the same f32
+    roundings)."""
+    m, n, k = 1000, 768, 1536
+    a, w = _operands(2100, m, n, k, torch.float16)
+    bias = orc.randn(2102, (n,), std=0.02)
+    gate = orc.randn(2103, (4, n), std=0.1)
+    res = orc.randn(2104, (m, n))
+    want = orc.gate_residual(res, orc.linear(a, w), gate, np.array([0, 250, 500, 750, m], np.int64), bias)
+    got = host(ops.linear_gate_residual(to_dev(a, dev, torch.float16), to_dev(w, dev, torch.float16), to_dev(res, dev),
+                                        bias=to_dev(bias, dev), gate=to_dev(gate, dev), rows_per_batch=250))
+    g_rows = np.repeat(np.abs(gate), 250, axis=0)
+    bound = _sum_bound(a, w) * g_rows + 2.0 ** -22 * np.maximum(np.abs(want), 1.0)
+    assert np.all(np.abs(got - want) <= bound)
+
+
+def test_gate_residual_ungated_no_bias_f16(dev):
+    """The cross join x += h + bias without a gate, and without a bias: f16
+    residual, the storage tolerance of tests/_parity.py."""
+    m, n, k = 513, 256, 512
+    a, w = _operands(2200, m, n, k, torch.float16)
+    res = storage_round(orc.randn(2201, (m, n)), torch.float16)
+    bias = orc.randn(2202, (n,), std=0.02)
+    ad, wd, rd = to_dev(a, dev, torch.float16), to_dev(w, dev, torch.float16), to_dev(res, dev, torch.float16)
+    assert_close(ops.linear_gate_residual(ad, wd, rd, bias=to_dev(bias, dev)),
+                 orc.gate_residual(res, orc.linear(a, w), None, None, bias), torch.float16, "ungated")
+    assert_close(ops.linear_gate_residual(ad, wd, rd), orc.gate_residual(res, orc.linear(a, w), None), torch.float16,
+                 "ungated, no bias")

@@ -588,6 +588,50 @@ int32_t t2h_linear(const void* x, int64_t ldx, const void* w, const float* bias,
     return hip_status(launch_gemm(a, static_cast<hipStream_t>(stream)), fn);
 }
 
+int32_t t2h_linear_gate_residual(const void* x, int64_t ldx, const void* w, const float* bias, const void* res,
+                                 void* out, int64_t ldo, int64_t rows, int32_t in_features, int32_t out_features,
+                                 int32_t dtype, int32_t out_dtype, const float* gate, int64_t gate_stride,
+                                 const int64_t* offsets, int32_t nbatch, int64_t rows_per_batch, void* stream) {
+    const char* fn = "t2h_linear_gate_residual";
+    if (dtype != T2H_F16 && dtype != T2H_BF16) return fail(T2H_EINVAL, "%s: operands must be f16 or bf16", fn);
+    if (out_dtype != T2H_F32 && out_dtype != dtype)
+        return fail(T2H_EINVAL, "%s: out_dtype must be f32 or the operand dtype", fn);
+    if (rows < 0 || in_features <= 0 || out_features <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
+    if (out_features % gemm_feature_tile() != 0)
+        return fail(T2H_EINVAL, "%s: out_features %d is not a multiple of %d", fn, out_features, gemm_feature_tile());
+    if (in_features % gemm_k_step() != 0)
+        return fail(T2H_EINVAL, "%s: in_features %d is not a multiple of %d", fn, in_features, gemm_k_step());
+    if (ldx < in_features || ldo < out_features) return fail(T2H_EINVAL, "%s: row stride below the row", fn);
+    if (ldx % 8 != 0 || ldo % (out_dtype == T2H_F32 ? 4 : 8) != 0)
+        return fail(T2H_EINVAL, "%s: ldx must be a multiple of 8, ldo of %d", fn, out_dtype == T2H_F32 ? 4 : 8);
+    if (gate != nullptr && gate_stride == 0) gate_stride = out_features;
+    if (gate != nullptr && gate_stride < out_features) return fail(T2H_EINVAL, "%s: gate_stride < out_features", fn);
+    if (int32_t rc = check_batch(offsets, nbatch, rows_per_batch, fn)) return rc;
+    if (rows == 0) return ok();
+    if (x == nullptr || w == nullptr || res == nullptr || out == nullptr) return fail(T2H_EINVAL, "%s: NULL tensor", fn);
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(res, 16) || !aligned(out, 16) ||
+        (bias != nullptr && !aligned(bias, 16)) || (gate != nullptr && (!aligned(gate, 16) || gate_stride % 4 != 0)))
+        return fail(T2H_EINVAL, "%s: misaligned tensor", fn);
+    GemmArgs a{};
+    a.x = x;
+    a.ldx = ldx;
+    a.w = w;
+    a.rows = rows;
+    a.n = out_features;
+    a.k = in_features;
+    a.dtype = dtype;
+    a.bias = bias;
+    a.act = T2H_ACT_NONE;
+    a.out = out;
+    a.ldo = ldo;
+    a.out_dtype = out_dtype;
+    a.res = res;
+    a.gate = gate;
+    a.gate_stride = gate_stride;
+    a.batch = BatchArgs{offsets, gate != nullptr ? nbatch : 0, rows_per_batch};
+    return hip_status(launch_gemm_residual(a, static_cast<hipStream_t>(stream)), fn);
+}
+
 int32_t t2h_gate_residual(const void* x, const void* h, void* out, const float* bias, const float* gate,
                           int64_t p_stride, int64_t rows, int32_t cols, int32_t dtype, const int64_t* offsets,
                           int32_t nbatch, int64_t rows_per_batch, void* stream) {

@@ -438,6 +438,140 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
     }
 }
 
+// ---- linear + gated residual: out = res + fl(fl(acc + bias) * gate[b(t)]) ----
+// The residual join of the block (x += (h + bias) * gate, or x += h + bias)
+// in the store of the GEMM that makes h, so h never reaches memory; the
+// rounding sequence is the gated-residual kernel's, with h = the f32 sums.
+// 16-bit outputs: the residual tile is copied into the freed LDS stages with
+// direct-to-LDS loads (each lane fetches the chunk that the staging swizzle
+// puts at its slot), each lane updates its values there in place, and whole
+// rows leave as 16-byte stores. f32 outputs read and write the residual
+// directly. out may alias res (every element is read before it is written,
+// by the same thread).
+template <typename T, typename O>
+__global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
+    TileOf tile;
+    if (!tile.init(a)) return;
+    const int64_t t0 = tile.t0, n0 = tile.n0;
+    f32x16 acc[kFI][kTJ];
+    zero_acc(acc);
+    gemm_mainloop<T>(a, t0, n0, lds, acc);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wf = wave & 1, wt = wave >> 1;
+    const int fr = lane & 31, h = lane >> 5;
+    const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
+    const O* __restrict__ res = static_cast<const O*>(a.res);
+    O* __restrict__ out = static_cast<O*>(a.out);
+    const int64_t last = a.rows - 1;
+    // gate row of the tile when all its rows share one batch (block-uniform),
+    // else -1: each token looks up its own
+    int64_t tile_b = 0;
+    if (a.gate != nullptr) {
+        const int64_t tl = t0 + kBT - 1 < last ? t0 + kBT - 1 : last;
+        const int32_t b0 = bm.batch_of(t0 < last ? t0 : last);
+        tile_b = bm.batch_of(tl) == b0 ? b0 : -1;
+    }
+    // bias and gate of feature group fi (4 runs of 4 features per lane)
+    auto params = [&](int fi, float (&bv)[4][4], float (&gv)[4][4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t n = n0 + wf * kWF + fi * 32 + q * 8 + h * 4;
+            if (a.bias != nullptr) load_params<4>(a.bias + n, bv[q]);
+            if (a.gate != nullptr && tile_b >= 0) load_params<4>(a.gate + tile_b * a.gate_stride + n, gv[q]);
+        }
+    };
+    // u = res + fl(fl(acc + bias) * gate) for token tile tj, group (fi, q)
+    auto join4 = [&](int fi, int tj, int q, const float* bq, const float* gq, const float* rv, float* u) {
+        float g[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) g[i] = gq[i];
+        if (a.gate != nullptr && tile_b < 0) {
+            const int64_t t = t0 + wt * kWT + tj * 32 + fr;
+            load_params<4>(a.gate + bm.batch_of(t < last ? t : last) * a.gate_stride + n0 + wf * kWF + fi * 32 +
+                               q * 8 + h * 4, g);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = a.bias != nullptr ? add_rn(acc[fi][tj][q * 4 + i], bq[i]) : acc[fi][tj][q * 4 + i];
+            if (a.gate != nullptr) v = mul_rn(v, g[i]);
+            u[i] = add_rn(rv[i], v);
+        }
+    };
+    if constexpr (sizeof(O) == 2) {
+        static_assert(kBT * kBF * 2 <= kStages * kStageBytes, "C tile fits the stage buffers");
+        constexpr int kRowsPerWave = kBT / 4;
+        // residual rows -> LDS: row r's chunk c at slot c ^ (r % 32); lane l
+        // of an instruction fills slot l % 32 of row 2 it + l / 32
+        const uint8_t* rb = static_cast<const uint8_t*>(a.res);
+#pragma unroll 4
+        for (int it = 0; it < kRowsPerWave / 2; ++it) {
+            const int r = wave * kRowsPerWave + it * 2 + h;
+            const int64_t t = t0 + r < last ? t0 + r : last;
+            const int c = fr ^ (r & 31);
+            __builtin_amdgcn_global_load_lds(rb + (t * a.ldo + n0 + c * 8) * 2,
+                                             lds + (wave * kRowsPerWave + it * 2) * (kBF * 2), 16, 0, 0);
+        }
+        wait_vm<0>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int fi = 0; fi < kFI; ++fi) {
+            float bv[4][4], gv[4][4];
+            params(fi, bv, gv);
+#pragma unroll
+            for (int tj = 0; tj < kTJ; ++tj) {
+                const int r = wt * kWT + tj * 32 + fr;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = (wf * kWF + fi * 32 + q * 8) / 8;
+                    u32x2* p = reinterpret_cast<u32x2*>(lds + r * (kBF * 2) + ((c ^ (r & 31)) * 16) + h * 8);
+                    const u32x2 w0 = *p;
+                    float rv[4], u[4];
+                    Word<O>::unpack(w0.x, rv);
+                    Word<O>::unpack(w0.y, rv + 2);
+                    join4(fi, tj, q, bv[q], gv[q], rv, u);
+                    u32x2 w;
+                    w.x = Word<O>::pack(u);
+                    w.y = Word<O>::pack(u + 2);
+                    *p = w;
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+#pragma unroll 4
+        for (int it = 0; it < kRowsPerWave / 2; ++it) {
+            const int r = wave * kRowsPerWave + it * 2 + h;
+            const int c = fr;
+            const int64_t t = t0 + r;
+            const u32x4 w = *reinterpret_cast<const u32x4*>(lds + r * (kBF * 2) + ((c ^ (r & 31)) * 16));
+            if (t < a.rows) *reinterpret_cast<u32x4*>(out + t * a.ldo + n0 + c * 8) = w;
+        }
+    } else {
+#pragma unroll
+        for (int fi = 0; fi < kFI; ++fi) {
+            float bv[4][4], gv[4][4];
+            params(fi, bv, gv);
+#pragma unroll
+            for (int tj = 0; tj < kTJ; ++tj) {
+                const int64_t t = t0 + wt * kWT + tj * 32 + fr;
+                if (t >= a.rows) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t n = n0 + wf * kWF + fi * 32 + q * 8 + h * 4;
+                    float rv[4], u[4];
+                    load_elems<O, 4>(res + t * a.ldo + n, rv);
+                    join4(fi, tj, q, bv[q], gv[q], rv, u);
+                    store_elems<O, 4>(out + t * a.ldo + n, u);
+                }
+            }
+        }
+    }
+}
+
 // ---- qkv linear + attention epilogue + head-major pack ----------------------
 // The qkv GEMM's output [rows, 3, H, 128] never reaches memory. A wave's 128
 // features are one head (q, k or v: head hg = n / 128, tensor hg / H, head
@@ -684,6 +818,14 @@ hipError_t gemm_typed(const GemmArgs& a, hipStream_t s) {
 }
 
 template <typename T>
+hipError_t gemm_res_typed(const GemmArgs& a, hipStream_t s) {
+    const dim3 g = grid_1d(a.nblocks), blk(kGemmThreads);
+    if (a.out_dtype == T2H_F32) hipLaunchKernelGGL((gemm_res_kernel<T, float>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((gemm_res_kernel<T, T>), g, blk, 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
 hipError_t qkv_typed(const GemmArgs& g, const PackArgs& p, const RopeSlots& tab, hipStream_t s) {
     const dim3 grid = grid_1d(g.nblocks), blk(kGemmThreads);
     if (p.k_transposed) hipLaunchKernelGGL((qkv_pack_kernel<T, true>), grid, blk, 0, s, g, p, tab);
@@ -702,6 +844,14 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.nblocks == 0) return hipSuccess;
     if (a.dtype == T2H_F16) return gemm_typed<_Float16>(a, s);
     return gemm_typed<__bf16>(a, s);
+}
+
+hipError_t launch_gemm_residual(GemmArgs a, hipStream_t s) {
+    a.ftiles = a.n / kBF;
+    a.nblocks = ((a.rows + kBT - 1) / kBT) * a.ftiles;
+    if (a.nblocks == 0) return hipSuccess;
+    if (a.dtype == T2H_F16) return gemm_res_typed<_Float16>(a, s);
+    return gemm_res_typed<__bf16>(a, s);
 }
 
 int32_t gemm_head_dim() { return kHead; }

@@ -120,6 +120,11 @@ struct GemmArgs {
     int32_t out_dtype;       // T2H_F32 or dtype
     int64_t nblocks;         // set by the launcher: token tiles x feature tiles
     int32_t ftiles;          // feature tiles
+    // residual epilogue (t2h_linear_gate_residual): out = res + fl(fl(acc + bias) * gate[b])
+    const void* res;         // [rows, n], rows ldo elements apart, out_dtype; may alias out
+    const float* gate;       // gate rows [nbatch, n] gate_stride apart, or nullptr (ungated)
+    int64_t gate_stride;
+    BatchArgs batch;
 };
 
 // Flow-matching Euler step (t2h_flow_euler_step).
@@ -197,6 +202,7 @@ int32_t gemm_feature_tile();   // output features per block (out_features must b
 int32_t gemm_k_step();         // k per stage (in_features must be a multiple)
 int32_t gemm_head_dim();       // head_dim of the fused qkv GEMM + pack
 hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, hipStream_t s);
+hipError_t launch_gemm_residual(GemmArgs a, hipStream_t s);
 // t2h_sampler.hip
 hipError_t launch_euler(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
 // t2h_eltwise.hip

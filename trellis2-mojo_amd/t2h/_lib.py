@@ -41,6 +41,8 @@ _SIGNATURES = {
     "t2h_activation": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_p],
     "t2h_qkv_linear_pack": [c_p, c_i64, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p, c_p, c_p, c_p, c_p, c_i32, c_p,
                             c_i32, c_i32, c_p, c_i64, c_p, c_i32, c_i32, c_p, c_i64, c_p, c_p, c_i64, c_i32, c_p],
+    "t2h_linear_gate_residual": [c_p, c_i64, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_p, c_i64,
+                                 c_p, c_i32, c_i64, c_p],
     "t2h_linear": [c_p, c_i64, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_p],
     "t2h_gate_residual": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_i32, c_p, c_i32, c_i64, c_p],
     "t2h_gate_residual_ln_modulate": [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_f32, c_i32, c_p, c_p, c_i64, c_i64,

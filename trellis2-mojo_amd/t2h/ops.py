@@ -431,6 +431,41 @@ def linear(x, weight, bias=None, act: int = ACT_NONE, out_dtype=None, out=None) 
     return out
 
 
+def linear_gate_residual(x, weight, res, bias=None, gate=None, offsets=None, rows_per_batch: int = 0,
+                         out=None) -> torch.Tensor:
+    """res + fl(fl(x @ weight^T + bias) * gate[b]) on the matrix cores (gate
+    None: res + fl(acc + bias)): x [rows, K] float16/bfloat16, weight [N, K]
+    of x's dtype, res [rows, N] of x's dtype or float32 (the output type);
+    gate rows [B, N] or [N] float32 with offsets / rows_per_batch as
+    gate_residual. out=res updates the residual stream in place."""
+    _dev(x, "linear_gate_residual")
+    _dev(weight, "linear_gate_residual")
+    _dev(res, "linear_gate_residual")
+    dt = _dtype(x, "linear_gate_residual")
+    if weight.dtype != x.dtype or weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("linear_gate_residual: weight must be a contiguous [N, K] tensor of x's dtype")
+    n, k = weight.shape
+    if x.dim() != 2 or x.shape[1] != k or x.stride(1) != 1:
+        raise ValueError("linear_gate_residual: x must be [rows, K] with unit column stride")
+    rows, ldx = x.shape[0], (x.stride(0) if x.shape[0] > 1 else k)
+    if res.dtype not in (x.dtype, torch.float32) or res.shape != (rows, n) or not res.is_contiguous():
+        raise ValueError("linear_gate_residual: res must be a contiguous [rows, N] tensor of x's dtype or float32")
+    if bias is not None:
+        _dev(bias, "linear_gate_residual")
+        if bias.dtype != torch.float32 or bias.numel() != n or not bias.is_contiguous():
+            raise ValueError("linear_gate_residual: bias must be a contiguous float32 [N] tensor")
+    gp, gs, ng = _param_rows(gate, n, "linear_gate_residual")
+    off, nb, rpb = _batch(offsets, rows_per_batch, ng, rows, "linear_gate_residual")
+    if out is None:
+        out = torch.empty_like(res)
+    elif out.dtype != res.dtype or out.shape != res.shape or not out.is_contiguous():
+        raise ValueError("linear_gate_residual: out must match res")
+    call("t2h_linear_gate_residual", x.data_ptr(), ldx, weight.data_ptr(), bias.data_ptr() if bias is not None else None,
+         res.data_ptr(), out.data_ptr(), n, rows, k, n, dt, _dtype(res, "linear_gate_residual"), gp, gs, off, nb, rpb,
+         _stream())
+    return out
+
+
 def gate_residual(x, h, gate=None, bias=None, offsets=None, rows_per_batch: int = 0, out=None) -> torch.Tensor:
     """x + fl(fl(h + bias) * gate[b]); x None -> the gated term alone."""
     rows, c = _rows_view(h, "gate_residual")
