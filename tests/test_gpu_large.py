@@ -143,3 +143,41 @@ def test_two_d_grid_sampler_rescale(dev):
     pred = orc.flow_rescale(xs, orc.flow_cfg(ps, ns, 3.0), ps, 0.8, 1e-5, 0.7)
     want = orc.flow_step(xs, pred, 0.8, 0.7)
     assert_close(xp[idx], want, torch.float32, "sampler on a 2-D grid")
+
+
+def test_linear_output_past_2g_elements(dev):
+    """The MFMA GEMM with an output of more than 2^31 elements ([466,000+,
+    4608] f16, 4.3 GB): sampled rows, including those straddling element 2^31,
+    match the oracle's GEMM on the same rows (to the f16 storage bar)."""
+    n, k = 4608, 256
+    rows = BIG // n + 517
+    x = _fill((rows, k), torch.float16, dev, 21)
+    w = (torch.randn((n, k), device=dev) * 0.05).to(torch.float16)
+    out = ops.linear(x, w)
+    assert out.numel() > BIG
+    idx = _rows(rows, n)
+    want = orc.linear(host(x[idx]), host(w))
+    assert_close(out[idx], want, torch.float16, "linear rows past 2^31 output elements")
+    del x, out
+    torch.cuda.empty_cache()
+
+
+def test_qkv_linear_pack_past_2g_elements(dev):
+    """The fused qkv linear + pack with qh/kt/vh of more than 2^31 elements
+    each (rows x 12 heads x 128 > 2^31): sampled tokens match the oracle's
+    GEMM followed by the attention epilogue and packs."""
+    h, d, k = 12, 128, 64
+    rows = BIG // (h * d) + 333
+    x = _fill((rows, k), torch.float16, dev, 22)
+    w = (torch.randn((3 * h * d, k), device=dev) * 0.1).to(torch.float16)
+    mp = (rows + 63) // 64 * 64
+    qh, kt, vh = ops.qkv_linear_pack(x, w, h, mp=mp, lp=mp, use_rope=False, k_transposed=True)
+    assert qh.numel() > BIG and kt.numel() > BIG
+    idx = _rows(rows, h * d)
+    qkv = orc.linear(host(x[idx]), host(w)).reshape(-1, 3, h, d)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    assert_close(qh[:, idx], (qkv[:, 0] * scale).transpose(1, 0, 2), torch.float16, "qh")
+    assert_close(kt[:, :, idx], qkv[:, 1].transpose(1, 2, 0), torch.float16, "kt")
+    assert_close(vh[:, idx], qkv[:, 2].transpose(1, 0, 2), torch.float16, "vh")
+    del x, qh, kt, vh
+    torch.cuda.empty_cache()
