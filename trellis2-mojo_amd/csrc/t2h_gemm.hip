@@ -18,14 +18,17 @@
 // rounded to f16, f32 accumulation; gpu/linear.mojo:326-388, selected by
 // GpuLinear.try_build 430-465); only the summation order differs.
 //
-// Tiling: a block of 4 waves computes 256 features x 128 tokens (2 x 2 waves
-// of 128 x 64, 8 MFMA tiles and 128 accumulators per lane). K advances in
-// steps of 32 through double-buffered LDS tiles whose rows are padded by 16
-// bytes (conflict-free 16-byte fragment reads); the next step's global loads
-// are in flight while the current step's MFMAs run. Tiles are numbered
-// token-tile major and the numbers are dealt to the 8 XCDs in contiguous
-// ranges, so the feature tiles of one token tile run on one XCD one after
-// the other and read its x rows from that XCD's L2.
+// Tiling: a block of 4 waves computes 256 features x 256 tokens (2 x 2 waves
+// of 128 x 128: 16 MFMA tiles and 256 accumulators per lane, one wave per
+// SIMD). K advances in steps of 64 through two 64 KB LDS stages filled by
+// direct-to-LDS loads (global_load_lds_dwordx4: a wave's 64 lanes fill one
+// contiguous KB); the 16-byte k chunks of each tile row are XOR-swizzled so
+// that the fragment reads are conflict-free. The next stage's loads are in
+// flight while the current stage's MFMAs run, and each substep's fragments
+// are read while the previous substep's MFMAs run. Tile numbers are dealt
+// to the 8 XCDs in contiguous ranges and walked in groups of a few token
+// tiles, feature tile by feature tile, so the blocks resident on one XCD
+// share a few weight and token slabs in its L2.
 //
 // Reference: GpuLinear.enqueue_gemm (gpu/linear.mojo:535-560, c[m, co] =
 // a[m, ci] @ W^T), the MLP's lin0 + gelu_tanh_bias (gpu/linear.mojo:662-684,
