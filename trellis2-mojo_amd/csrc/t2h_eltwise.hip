@@ -84,6 +84,19 @@ __device__ __forceinline__ bool tile_of(const EltArgs& a, Tile& t) {
 
 // ---- activation(x + bias) ----------------------------------------------------
 
+// Stores the tile's rows after all of them are computed. Loads and stores
+// share vmcnt on gfx9, so a load consumed while a store is pending waits for
+// vmcnt(0), i.e. for the store to complete; the per-batch parameter loads of
+// the row loop therefore all come before the first store.
+template <typename T, int V>
+__device__ __forceinline__ void store_rows(T* __restrict__ o, int64_t cols, const Tile& t, const float (&v)[kRpt][V]) {
+#pragma unroll
+    for (int k = 0; k < kRpt; ++k) {
+        if (k >= t.nrows) break;
+        st<T, V>(o + (t.r0 + k) * cols + t.col0, v[k]);
+    }
+}
+
 template <typename T, int V, int KIND, bool BIAS>
 __global__ __launch_bounds__(1024) void act_kernel(EltArgs a) {
     Tile t;
@@ -143,8 +156,8 @@ __global__ __launch_bounds__(1024) void gate_res_kernel(EltArgs a) {
             if (a.gate) u = mul_rn(u, g[i]);
             hv[k][i] = x ? add_rn(xv[k][i], u) : u;
         }
-        st<T, V>(o + r * a.cols + t.col0, hv[k]);
     }
+    store_rows<T, V>(o, a.cols, t, hv);
 }
 
 // ---- out = fl(fl(x * fl(1 + scale[b])) + shift[b]) ---------------------------
@@ -174,8 +187,8 @@ __global__ __launch_bounds__(1024) void modulate_kernel(EltArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < V; ++i) v[k][i] = add_rn(mul_rn(v[k][i], sc1[i]), sh[i]);
-        st<T, V>(o + r * a.cols + t.col0, v[k]);
     }
+    store_rows<T, V>(o, a.cols, t, v);
 }
 
 // ---- out = x OP other[b] (other row of cols, or one scalar per batch) ---------
@@ -221,8 +234,8 @@ __global__ __launch_bounds__(1024) void binop_kernel(EltArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < V; ++i) v[k][i] = apply_op(v[k][i], ov[i], a.kind);
-        st<T, V>(o + r * a.cols + t.col0, v[k]);
     }
+    store_rows<T, V>(o, a.cols, t, v);
 }
 
 // ---- timestep embedding --------------------------------------------------------

@@ -65,14 +65,29 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
     const bool live = r < a.rows;
     if (which == 2) {                      // packed qkv: v += bias_v (block-uniform branch)
         if (!live) return;
+        // the q/k lane layout over the row's heads; every load before the
+        // first store (loads and stores share vmcnt on gfx9)
         T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
-        for (int e0 = lane * VE; e0 < HD; e0 += 64 * VE) {
-            float vv[VE], bv[VE];
-            load_elems<T, VE>(vr + e0, vv);
-            load_params<VE>(a.bias_v + e0, bv);
+        float vv[NG][E];
 #pragma unroll
-            for (int i = 0; i < VE; ++i) vv[i] = add_rn(vv[i], bv[i]);
-            store_elems<T, VE>(vr + e0, vv);
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+            L::load(vr + (int64_t)(hh < H ? hh : H - 1) * D, m, vv[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+            if (hh < H) {
+                float bv[E];
+                L::params(a.bias_v + (int64_t)hh * D, m, bv);
+#pragma unroll
+                for (int i = 0; i < E; ++i) vv[it][i] = add_rn(vv[it][i], bv[i]);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < NG; ++it) {
+            const int hh = 4 * it + g;
+            if (hh < H) L::store(vr + (int64_t)hh * D, m, vv[it]);
         }
         return;
     }
