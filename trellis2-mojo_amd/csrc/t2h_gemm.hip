@@ -267,10 +267,31 @@ struct TileOf {
     }
 };
 
+// Residual rows of a 16-bit gated-residual tile into LDS: 32 rows per wave
+// from `row0` (row r at r * 512 bytes, chunk c at slot c ^ (r % 32), the
+// epilogue's staging layout), 2 rows per direct-to-LDS load: lane l fills
+// slot l % 32 of row 2 it + l / 32. Rows past the last token read the last.
+__device__ __forceinline__ void res_rows(const GemmArgs& a, int64_t t0, int64_t n0, uint8_t* lds, int row0, int wave,
+                                         int lane) {
+    const uint8_t* rb = static_cast<const uint8_t*>(a.res);
+    const int64_t last = a.rows - 1;
+    const int fr = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int r = row0 + wave * 32 + it * 2 + h;
+        const int64_t t = t0 + r < last ? t0 + r : last;
+        const int c = fr ^ (r & 31);
+        __builtin_amdgcn_global_load_lds(rb + (t * a.ldo + n0 + c * 8) * 2,
+                                         lds + (row0 + wave * 32 + it * 2) * (kBF * 2), 16, 0, 0);
+    }
+}
+
 // The block's accumulators acc[t0.., n0..] over all of k. On return every
 // wave has finished reading the LDS stages (a barrier follows the last one),
-// so the caller may reuse the LDS.
-template <typename T>
+// so the caller may reuse the LDS. RES_PRE: the last stage's MFMAs also
+// cover the residual rows of the stage buffer it leaves free (rows
+// [128 * (ksteps % 2), +128) of a 16-bit gated-residual tile).
+template <typename T, bool RES_PRE = false>
 __device__ __forceinline__ void gemm_mainloop(const GemmArgs& a, int64_t t0, int64_t n0, uint8_t* lds,
                                               f32x16 (&acc)[kFI][kTJ]) {
     using V8 = typename Mfma<T>::v8;
@@ -340,6 +361,12 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& a, int64_t t0, int
     if (kStages > 3 && r >= 4) stage_body<T, true, false, (kStages > 3 ? 2 : 0)>(acc, af, bf, cx, ks++);
     if (kStages > 2 && r >= 3) stage_body<T, true, false, (kStages > 2 ? 1 : 0)>(acc, af, bf, cx, ks++);
     if (r >= 2) stage_body<T, true, false, 0>(acc, af, bf, cx, ks++);
+    if constexpr (RES_PRE) {
+        // stage ks + 1's buffer: no load targets it any more and every wave
+        // finished reading it before the barrier of stage ks - 1
+        static_assert(kStages == 2 && kStageBytes == 128 * kBF * 2, "a free stage holds 128 residual rows");
+        res_rows(a, t0, n0, lds, ((ks + 1) % kStages) * 128, wave, lane);
+    }
     stage_body<T, false, false, 0>(acc, af, bf, cx, ks);
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();                // every wave is done reading the stages
@@ -447,20 +474,17 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
 // rounding sequence is the gated-residual kernel's, with h = the f32 sums.
 // 16-bit outputs: the residual tile is copied into the freed LDS stages with
 // direct-to-LDS loads (each lane fetches the chunk that the staging swizzle
-// puts at its slot), each lane updates its values there in place, and whole
-// rows leave as 16-byte stores. f32 outputs read and write the residual
-// directly. out may alias res (every element is read before it is written,
-// by the same thread).
+// puts at its slot; the half that lands in the stage buffer the last k step
+// leaves free is requested before that step's MFMAs), each lane updates its
+// values there in place, and whole rows leave as 16-byte stores. f32 outputs
+// read and write the residual directly. out may alias res (every element is
+// read before it is written, by the same thread).
 template <typename T, typename O>
 __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
     TileOf tile;
     if (!tile.init(a)) return;
     const int64_t t0 = tile.t0, n0 = tile.n0;
-    f32x16 acc[kFI][kTJ];
-    zero_acc(acc);
-    gemm_mainloop<T>(a, t0, n0, lds, acc);
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int wf = wave & 1, wt = wave >> 1;
@@ -471,6 +495,9 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(Ge
     const int64_t last = a.rows - 1;
     // gate row of the tile when all its rows share one batch (block-uniform),
     // else -1: each token looks up its own
+    f32x16 acc[kFI][kTJ];
+    zero_acc(acc);
+    gemm_mainloop<T, sizeof(O) == 2>(a, t0, n0, lds, acc);
     int64_t tile_b = 0;
     if (a.gate != nullptr) {
         const int64_t tl = t0 + kBT - 1 < last ? t0 + kBT - 1 : last;
@@ -506,24 +533,18 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(Ge
     if constexpr (sizeof(O) == 2) {
         static_assert(kBT * kBF * 2 <= kStages * kStageBytes, "C tile fits the stage buffers");
         constexpr int kRowsPerWave = kBT / 4;
-        // residual rows -> LDS: row r's chunk c at slot c ^ (r % 32); lane l
-        // of an instruction fills slot l % 32 of row 2 it + l / 32
-        const uint8_t* rb = static_cast<const uint8_t*>(a.res);
-#pragma unroll 4
-        for (int it = 0; it < kRowsPerWave / 2; ++it) {
-            const int r = wave * kRowsPerWave + it * 2 + h;
-            const int64_t t = t0 + r < last ? t0 + r : last;
-            const int c = fr ^ (r & 31);
-            __builtin_amdgcn_global_load_lds(rb + (t * a.ldo + n0 + c * 8) * 2,
-                                             lds + (wave * kRowsPerWave + it * 2) * (kBF * 2), 16, 0, 0);
-        }
+        // residual rows -> LDS: the last stage left rows [128 * (ksteps % 2),
+        // +128) loading; now the other half, and every bias and gate value
+        // of the lane, all in flight together
+        res_rows(a, t0, n0, lds, (1 - (a.k / kBK) % 2) * 128, wave, lane);
+        float bv[kFI][4][4], gv[kFI][4][4];
+#pragma unroll
+        for (int fi = 0; fi < kFI; ++fi) params(fi, bv[fi], gv[fi]);
         wait_vm<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int fi = 0; fi < kFI; ++fi) {
-            float bv[4][4], gv[4][4];
-            params(fi, bv, gv);
 #pragma unroll
             for (int tj = 0; tj < kTJ; ++tj) {
                 const int r = wt * kWT + tj * 32 + fr;
@@ -535,7 +556,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(Ge
                     float rv[4], u[4];
                     Word<O>::unpack(w0.x, rv);
                     Word<O>::unpack(w0.y, rv + 2);
-                    join4(fi, tj, q, bv[q], gv[q], rv, u);
+                    join4(fi, tj, q, bv[fi][q], gv[fi][q], rv, u);
                     u32x2 w;
                     w.x = Word<O>::pack(u);
                     w.y = Word<O>::pack(u + 2);
@@ -554,21 +575,31 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(Ge
             if (t < a.rows) *reinterpret_cast<u32x4*>(out + t * a.ldo + n0 + c * 8) = w;
         }
     } else {
+        // per feature group: its residual values and parameters are all
+        // loaded before its first store (loads and stores share vmcnt on
+        // gfx9: a load consumed while a store is pending waits for the store)
 #pragma unroll
         for (int fi = 0; fi < kFI; ++fi) {
             float bv[4][4], gv[4][4];
             params(fi, bv, gv);
+            float rv[kTJ][4][4];
+#pragma unroll
+            for (int tj = 0; tj < kTJ; ++tj) {
+                const int64_t t = t0 + wt * kWT + tj * 32 + fr;
+                const int64_t tc = t < a.rows ? t : last;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    load_elems<O, 4>(res + tc * a.ldo + n0 + wf * kWF + fi * 32 + q * 8 + h * 4, rv[tj][q]);
+            }
 #pragma unroll
             for (int tj = 0; tj < kTJ; ++tj) {
                 const int64_t t = t0 + wt * kWT + tj * 32 + fr;
                 if (t >= a.rows) continue;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int64_t n = n0 + wf * kWF + fi * 32 + q * 8 + h * 4;
-                    float rv[4], u[4];
-                    load_elems<O, 4>(res + t * a.ldo + n, rv);
-                    join4(fi, tj, q, bv[q], gv[q], rv, u);
-                    store_elems<O, 4>(out + t * a.ldo + n, u);
+                    float u[4];
+                    join4(fi, tj, q, bv[q], gv[q], rv[tj][q], u);
+                    store_elems<O, 4>(out + t * a.ldo + n0 + wf * kWF + fi * 32 + q * 8 + h * 4, u);
                 }
             }
         }
