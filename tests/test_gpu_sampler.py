@@ -93,6 +93,32 @@ def test_step_rescale_varlen_config4(dev, dtype):
     assert max_err(x0, storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
 
 
+def test_step_odd_rows_and_unaligned_state(dev):
+    """Rows of 12,289 elements (statistics blocks of 4,096 elements that
+    straddle rows and end in a 1-element tail), and the same state viewed one
+    element into its buffer (no 16-byte alignment): the oracle's bits without
+    rescale and its tolerance with it."""
+    shape = (3, 12289)
+    x, pos, neg = _case(3400, shape)
+    t, tp = 0.83, 0.77
+    pred = orc.flow_cfg(pos, neg, 4.0)
+    want = orc.flow_rescale(x, pred, pos, t, SM, 0.6)
+    cc = float(np.float32(SM + (1 - SM) * t))
+    for off in (0, 1):
+        bufs = []
+        for a in (x, pos, neg):
+            b = torch.zeros(a.size + off, dtype=torch.float32, device=dev)
+            b[off:] = to_dev(a.reshape(-1), dev)
+            bufs.append(b[off:].reshape(shape))
+        xp, x0 = ops.flow_euler_step(bufs[0], bufs[1], t, tp, SM, v_neg=bufs[2], guidance_strength=4.0)
+        assert _bits(xp, orc.flow_step(x, pred, t, tp), torch.float32)
+        assert _bits(x0, orc.flow_v_to_xstart(x, pred, t, SM), torch.float32)
+        xp, x0 = ops.flow_euler_step(bufs[0], bufs[1], t, tp, SM, v_neg=bufs[2], guidance_strength=4.0,
+                                     guidance_rescale=0.6)
+        assert max_err(x0, orc.flow_v_to_xstart(x, want, t, SM)) <= 1e-5
+        assert max_err(xp, orc.flow_step(x, want, t, tp)) <= 1e-5 / cc
+
+
 def test_step_rescale_uncovered_rows_and_workspace_reuse(dev):
     """Rows outside the token segments keep a zero prediction (x_prev = x,
     pred_x0 = x * a, bit-exact); one workspace serves consecutive calls."""
