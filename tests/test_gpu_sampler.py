@@ -94,10 +94,10 @@ def test_step_rescale_varlen_config4(dev, dtype):
 
 
 def test_step_odd_rows_and_unaligned_state(dev):
-    """Rows of 12,289 elements (statistics blocks of 4,096 elements that
-    straddle rows and end in a 1-element tail), and the same state viewed one
-    element into its buffer (no 16-byte alignment): the oracle's bits without
-    rescale and its tolerance with it."""
+    """Rows of 12,289 elements (three 4,096-element statistics blocks and a
+    1-element tail block per row, rows starting at odd element offsets), and
+    the same state viewed one element into its buffer (no 16-byte
+    alignment): the oracle's bits without rescale and its tolerance with it."""
     shape = (3, 12289)
     x, pos, neg = _case(3400, shape)
     t, tp = 0.83, 0.77
