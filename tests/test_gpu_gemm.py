@@ -174,3 +174,27 @@ def test_gate_residual_ungated_no_bias_f16(dev):
                  orc.gate_residual(res, orc.linear(a, w), None, None, bias), torch.float16, "ungated")
     assert_close(ops.linear_gate_residual(ad, wd, rd), orc.gate_residual(res, orc.linear(a, w), None), torch.float16,
                  "ungated, no bias")
+
+
+@pytest.mark.parametrize("k", [64, 128, 192])
+def test_one_two_three_k_steps_bit_exact(dev, k):
+    """1, 2 and 3 k steps of 64 (the pipelines' prologue and tails, and the
+    stage buffer the last step leaves free for the residual rows, which
+    alternates with the step count): integer operands, bit-exact, for the
+    linear (f32 and 16-bit out) and the gated residual (f16 and f32 streams)."""
+    m, n = 300, 512
+    rng, a, w = _int_case(30 + k, m, n, k, -2, 3)
+    bias = rng.integers(-3, 4, (n,)).astype(np.float32)
+    ad, wd = to_dev(a, dev, torch.float16), to_dev(w, dev, torch.float16)
+    want = orc.linear(a, w, bias=bias)
+    assert np.abs(want).max() < 256
+    assert np.array_equal(host(ops.linear(ad, wd, bias=to_dev(bias, dev), out_dtype=torch.float32)), want)
+    assert np.array_equal(host(ops.linear(ad, wd, bias=to_dev(bias, dev))), want)
+    gate = (2.0 ** rng.integers(-2, 2, (1, n))).astype(np.float32)
+    res = rng.integers(-8, 9, (m, n)).astype(np.float32)
+    offsets = np.array([0, m], np.int64)
+    want_r = orc.gate_residual(res, orc.linear(a, w), gate, offsets, bias)
+    assert np.abs(want_r).max() < 256
+    args = dict(bias=to_dev(bias, dev), gate=to_dev(gate, dev), offsets=to_dev(offsets, dev))
+    assert np.array_equal(host(ops.linear_gate_residual(ad, wd, to_dev(res, dev, torch.float16), **args)), want_r)
+    assert np.array_equal(host(ops.linear_gate_residual(ad, wd, to_dev(res, dev), **args)), want_r)
