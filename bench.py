@@ -97,7 +97,8 @@ class Chain:
             "gate_residual": 3 * T * C * e + C * 4,
             "copy": 2 * T * F * e,
         }
-        self.chain_bytes = (6144 + 12304 + 24576 + 9216) * T   # BASELINE.md byte model
+        # algorithmic bytes per token: LN+modulate, QK RMSNorm+RoPE, GELU+bias, gated residual
+        self.chain_bytes = (6144 + 12304 + 24576 + 9216) * T
 
     def op(self, name):
         o = self.ops
@@ -406,7 +407,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (the per-token ops are row-"
-              f"independent; see DESIGN.md for how rows would shard). Got --gpus {args.gpus}.", file=sys.stderr)
+              f"independent: each GPU would take a contiguous range of rows, with no exchange). "
+              f"Got --gpus {args.gpus}.", file=sys.stderr)
         sys.exit(2)
     import torch
 
@@ -474,9 +476,7 @@ def main():
     if args.all_configs:
         log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
         other = other_configs(torch, dev)
-        with open(os.path.join(ROOT, "gpurun_out", "configs.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out"))
-                  else os.devnull, "w") as f:
-            json.dump(other, f, indent=1)
+        log("configs 1-4 as JSON: " + json.dumps(other))
 
     out = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

@@ -288,7 +288,7 @@ struct TileOf {
 // writing it. Chunk i of wave w is the 1 KB at (i*kWaves + w) KB of a stage,
 // lane l's 16 bytes at l * 16.
 __device__ __forceinline__ constexpr int rs_lo(int s) { return kLoads * s / (kSub - 1); }
-__device__ __forceinline__ void rs_load(u32x4 (&r)[kLoads], const uint8_t* wbase, const uint8_t* xbase,
+__device__ __forceinline__ void rs_fetch(u32x4 (&r)[kLoads], const uint8_t* wbase, const uint8_t* xbase,
                                         const int64_t* src, int ks, int lo, int hi) {
     const int64_t ko = (int64_t)ks * kBK * 2;
 #pragma unroll
@@ -296,7 +296,7 @@ __device__ __forceinline__ void rs_load(u32x4 (&r)[kLoads], const uint8_t* wbase
         if (i >= lo && i < hi)
             r[i] = *reinterpret_cast<const u32x4*>((i < kLoadsA ? wbase : xbase) + src[i] + ko);
 }
-__device__ __forceinline__ void rs_store(const u32x4 (&r)[kLoads], uint8_t* st, int wave, int lane, int lo, int hi) {
+__device__ __forceinline__ void rs_write(const u32x4 (&r)[kLoads], uint8_t* st, int wave, int lane, int lo, int hi) {
 #pragma unroll
     for (int i = 0; i < kLoads; ++i)
         if (i >= lo && i < hi) *reinterpret_cast<u32x4*>(st + (i * kWaves + wave) * 1024 + lane * 16) = r[i];
@@ -338,8 +338,8 @@ __device__ __forceinline__ void stage_body_rs(f32x16 (&acc)[kFI][kTJ], typename 
         const bool last = s + 1 == kSub;
         if (!last) {
             read_frags<T>(af[n], bf[n], st, cx.fa, cx.fb, cx.slot ^ (32 * (s + 1)));
-            if (WRITE) rs_store(r, nst, cx.wave, lane, rs_lo(s), rs_lo(s + 1));
-            if (LOAD) rs_load(r, cx.wbase, cx.xbase, cx.src, ks + 2, rs_lo(s), rs_lo(s + 1));
+            if (WRITE) rs_write(r, nst, cx.wave, lane, rs_lo(s), rs_lo(s + 1));
+            if (LOAD) rs_fetch(r, cx.wbase, cx.xbase, cx.src, ks + 2, rs_lo(s), rs_lo(s + 1));
         } else if (NEXT) {
             __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's writes landed
             __builtin_amdgcn_s_barrier();
@@ -432,9 +432,9 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& a, int64_t t0, int
     if constexpr (kRegStaged) {
         static_assert(kStages == 2, "two buffers");
         u32x4 r[kLoads];
-        rs_load(r, wbase, xbase, src, 0, 0, kLoads);
-        rs_store(r, lds, wave, lane, 0, kLoads);
-        if (ksteps > 1) rs_load(r, wbase, xbase, src, 1, 0, kLoads);
+        rs_fetch(r, wbase, xbase, src, 0, 0, kLoads);
+        rs_write(r, lds, wave, lane, 0, kLoads);
+        if (ksteps > 1) rs_fetch(r, wbase, xbase, src, 1, 0, kLoads);
         __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         V8 af[2][kFI], bf[2][kTJ];
