@@ -38,6 +38,39 @@ constexpr int kPackRows = 64;
 constexpr int kPackBlock = 256;
 constexpr int kPackIters = kPackRows / 16;   // row groups of 4 per wave
 
+// One lane's E elements of one head row, held as the loaded 32-bit words so
+// that a prefetch stays in flight until the words are unpacked.
+template <typename T, int D>
+struct RawRow {
+    using L = HeadLanes<T, D>;
+    static constexpr int WP = L::VE * (int)sizeof(T) / 4;   // words per piece
+    static_assert(WP == 2 || WP == 4, "piece width");
+    uint32_t w[L::NC * WP];
+    __device__ __forceinline__ void load(const T* head, int m) {
+#pragma unroll
+        for (int j = 0; j < L::NC; ++j) {
+            const T* p = head + L::piece(m, j);
+            if constexpr (WP == 4) {
+                const u32x4 q = T2H_NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p))
+                                       : *reinterpret_cast<const u32x4*>(p);
+                w[j * 4 + 0] = q.x;
+                w[j * 4 + 1] = q.y;
+                w[j * 4 + 2] = q.z;
+                w[j * 4 + 3] = q.w;
+            } else {
+                const u32x2 q = T2H_NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p))
+                                       : *reinterpret_cast<const u32x2*>(p);
+                w[j * 2 + 0] = q.x;
+                w[j * 2 + 1] = q.y;
+            }
+        }
+    }
+    __device__ __forceinline__ void unpack(float* v) const {
+#pragma unroll
+        for (int k = 0; k < L::NC * WP; ++k) Word<T>::unpack(w[k], v + k * Word<T>::N);
+    }
+};
+
 // The 1-D grid covers row tiles x tensors x head groups, head groups varying
 // fastest. which[] maps the tensor index to the tensor a block packs
 // (0 = q, 1 = k, 2 = v); a block loops over the `hpb` heads of its group, so
@@ -109,12 +142,23 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
         }
     }
 
+    // The transposed path fetches head z + 1 before it stores head z, so a
+    // block's loads overlap its own stores.
+    RawRow<T, D> raw[kPackIters];
+    auto fetch = [&](int z) {
+        if (a.rows > 0) {
+#pragma unroll
+            for (int it = 0; it < kPackIters; ++it) raw[it].load(in + rl[it] * a.in_stride + (int64_t)z * D, m);
+        }
+    };
+    if constexpr (KT) fetch(hg * order.hpb);
     for (int zi = 0; zi < order.hpb; ++zi) {
         const int z = hg * order.hpb + zi;
+        if constexpr (!KT) fetch(z);
         float v[kPackIters][E];
         if (a.rows > 0) {
 #pragma unroll
-            for (int it = 0; it < kPackIters; ++it) L::load(in + rl[it] * a.in_stride + (int64_t)z * D, m, v[it]);
+            for (int it = 0; it < kPackIters; ++it) raw[it].unpack(v[it]);
         } else {
 #pragma unroll
             for (int it = 0; it < kPackIters; ++it)
@@ -164,6 +208,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
         }
         if constexpr (KT) {
             __syncthreads();
+            if (zi + 1 < order.hpb) fetch(z + 1);
             constexpr int VE = kPack<T>;            // elements per 16-byte vector
             constexpr int VPR = kPackRows / VE;     // vectors per output row (one e)
             for (int vi = threadIdx.x; vi < D * VPR; vi += kPackBlock) {
