@@ -787,7 +787,7 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_ne
         a.ratio = reinterpret_cast<float*>(static_cast<char*>(workspace) + blocks * 32);
         a.nblocks = blocks;
     } else {
-        a.nblocks = (n + kEulerChunk - 1) / kEulerChunk;
+        a.nblocks = (n + kEulerChunkPlain - 1) / kEulerChunkPlain;
     }
     return hip_status(launch_euler(a, blocks, cover_lo, cover_hi, static_cast<hipStream_t>(stream)), fn);
 }

@@ -128,7 +128,8 @@ struct GemmArgs {
 };
 
 // Flow-matching Euler step (t2h_flow_euler_step).
-constexpr int kEulerChunk = 4096;   // elements per block
+constexpr int kEulerChunk = 4096;        // elements per block of the rescale's two passes
+constexpr int kEulerChunkPlain = 2048;   // elements per block without the rescale
 constexpr int kEulerMaxSeg = 64;    // varlen segments carried in the kernel arguments
 struct EulerArgs {
     const void* x;

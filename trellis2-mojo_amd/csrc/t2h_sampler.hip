@@ -154,8 +154,8 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
     if (a.mode == 2) {
         SegMap::locate(a, b, s, lo, hi);
     } else {
-        lo = b * kEulerChunk;
-        hi = min(lo + kEulerChunk, a.n);
+        lo = b * kEulerChunkPlain;
+        hi = min(lo + kEulerChunkPlain, a.n);
     }
     const float ratio = a.mode == 2 ? a.ratio[s] : 0.0f;
     for (int64_t e = lo + threadIdx.x; e < hi; e += kEulerBlock) {
