@@ -52,6 +52,25 @@ def test_integer_operands_bit_exact(dev, dtype):
     assert np.array_equal(host(out16), want16)
 
 
+@pytest.mark.parametrize("out_dtype,act", [(torch.float32, None), (torch.float16, ops.ACT_RELU)])
+def test_more_tiles_than_cus_bit_exact(dev, out_dtype, act):
+    """66 token tiles (the last one ragged: 16740 = 65 * 256 + 100) x 7
+    feature tiles = 462 tiles: more than one per CU, and a count that is not
+    a multiple of 8, so the XCD deal of the tile numbers has unequal ranges.
+    Integer operands and bias, |sums| <= 772, so f32 and f16 outputs (ReLU
+    keeps integers) equal the oracle bit for bit."""
+    rng = np.random.default_rng(23)
+    m, n, k = 16740, 1792, 192
+    a = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    w = rng.integers(-2, 3, (n, k)).astype(np.float32)
+    b = rng.integers(-4, 5, (n,)).astype(np.float32)
+    out = ops.linear(to_dev(a, dev, torch.float16), to_dev(w, dev, torch.float16), bias=to_dev(b, dev),
+                     act=ops.ACT_NONE if act is None else act, out_dtype=out_dtype)
+    want = orc.linear(a, w, bias=b, act=act)
+    assert out.dtype == out_dtype
+    assert np.array_equal(host(out), want)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [1, 129, 1000])
 def test_random_operands_within_sum_bound(dev, dtype, m):
