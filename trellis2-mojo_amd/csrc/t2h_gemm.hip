@@ -1,10 +1,16 @@
 // The qkv linear fused with the self-attention epilogue and the head-major
-// pack (t2h_qkv_linear_pack), on the 4-wave layout of the GEMM core (tiling
-// and pipeline: t2h_gemm_core.h): a wave's 128 features are one head.
+// pack (t2h_qkv_linear_pack), on the GEMM core (tiling and pipeline:
+// t2h_gemm_core.h): a wave's 128 features are one head. T2H_QKV_WAVES picks
+// the layout: 8 (shipped; 64 tokens per wave, 128 accumulators, 10 % faster
+// on the config-5 qkv) or 4 (128 tokens per wave, direct-to-LDS loads).
 //
 // Reference: the qkv enqueue_gemm + bias_rms_rope_qkv + pack_q_z + pack_kv_z
 // of the self-attention chain (gpu/attention.mojo:507-563, 566-594, 634-662,
 // sequence 983-1013).
+#ifndef T2H_QKV_WAVES
+#define T2H_QKV_WAVES 8
+#endif
+#define T2H_GEMM_WAVES T2H_QKV_WAVES
 #include "t2h_gemm_core.h"
 
 namespace t2h {
@@ -19,13 +25,22 @@ namespace {
 // x * rsqrt(sum x^2) * (gamma * sqrt(D)); q/k: RoPE on the in-lane pairs
 // (2p, 2p + 1) with cos/sin from the phase table or from the token's
 // position; q: * 1/sqrt(D); tokens >= rows: 0. The head then goes through
-// the wave's own 16 KB of LDS, 64 tokens at a time, as 256-byte token rows
-// and leaves as 16-byte vectors: whole token rows (qh [H, mp, D], k [H, lp,
-// D], vh [H, lp, D]) or, for the transposed k [H, D, lp], 8 tokens of one
-// feature gathered from 8 rows. Tiles past the last token row skip the GEMM
-// and write the pads.
+// the wave's own LDS region (kStaged tokens at a time: 64 with 4 waves, 32
+// with 8, 16 KB or 8 KB) as 256-byte token rows and leaves as 16-byte
+// vectors: whole token rows (qh [H, mp, D], k [H, lp, D], vh [H, lp, D]) or,
+// for the transposed k [H, D, lp], 8 tokens of one feature gathered from 8
+// rows. Tiles past the last token row skip the GEMM and write the pads.
 constexpr int kHead = 128;
 static_assert(kTJ == 2 || kTJ == 4, "copy_col cases");
+constexpr int kStaged = kWaves == 8 ? 32 : 64;   // token rows a wave stages at a time
+constexpr int kJJ = kStaged / 32;                // token tiles per staged group
+constexpr int kRegion = kStaged * 256;           // bytes of a wave's staging region
+constexpr int kParamOff = kWaves * kRegion;      // [head][bias, gamma * sqrt(D)][128] f32
+constexpr int kPPT = 2 * 2 * kHead / kGemmThreads;   // parameters per thread
+// 8 waves unroll their two groups, so that each group's accumulators are used
+// in place and are dead after it (128 accumulators in 256 registers); 4 waves
+// keep the loop (a runtime token tile picks its accumulators by a switch).
+constexpr int kGrpUnroll = kWaves == 8 ? kTJ / kJJ : 1;
 
 // Slot of a 16-byte chunk in a staged 256-byte token row: chunk c of row r
 // at c ^ stage_swz(r). Over 32 consecutive rows (one row-major write) every
@@ -43,13 +58,14 @@ __device__ __forceinline__ void copy_col(const f32x16 (&acc)[kFI][kTJ], float (&
 
 template <typename T, bool KT>
 __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(GemmArgs g, PackArgs p, RopeSlots tab) {
-    // One LDS array: the GEMM's stages, then the epilogue's staging (4 waves
-    // x 16 KB: 64 token rows of 256 bytes) and the tile's parameters at 64 KB.
-    // (A separate parameter array that took the kernel past 128 KB of LDS
-    // measured 20 % slower on MI355X.)
+    // One LDS array: the GEMM's stages, then the epilogue's staging (a
+    // region per wave) and the tile's parameters at 64 KB. (A separate
+    // parameter array that took the kernel past 128 KB of LDS measured 20 %
+    // slower on MI355X.)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
-    static_assert(kWF == kHead && kWT % 64 == 0 && 4 * 64 * 256 + 2 * 2 * kHead * 4 <= kStages * kStageBytes,
+    static_assert(kWF == kHead && kWT % kStaged == 0 && kParamOff + 2 * 2 * kHead * 4 <= kStages * kStageBytes,
                   "staging layout");
+    static_assert(kPPT * kGemmThreads == 2 * 2 * kHead, "parameters per thread");
     TileOf tile;
     if (!tile.init(g)) return;
     const int64_t t0 = tile.t0, n0 = tile.n0;
@@ -64,19 +80,27 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
     const float* __restrict__ bias = which == 0 ? p.bias_q : which == 1 ? p.bias_k : p.bias_v;
     const float* __restrict__ gamma = which == 0 ? p.gamma_q : which == 1 ? p.gamma_k : nullptr;
 
-    // the tile's bias and gamma * sqrt(D) (one value of each per thread) are
-    // requested before the GEMM and land in LDS after it
-    static_assert(kGemmThreads == 2 * kHead, "one parameter per thread and head");
-    const int ph_ = threadIdx.x / kHead, pd_ = threadIdx.x % kHead;
-    const int pz_ = (int)((n0 + ph_ * kWF) / kHead) - which * p.heads;
-    const float pbias = bias != nullptr ? bias[pz_ * kHead + pd_] : 0.0f;
-    const float pgam = gamma != nullptr ? gamma[pz_ * kHead + pd_] : 0.0f;
+    // the tile's bias and gamma * sqrt(D) (slot i = (head * 2 + kind) * 128 +
+    // d, kPPT slots per thread) are requested before the GEMM and land in LDS
+    // after it
+    float pv[kPPT];
+#pragma unroll
+    for (int j = 0; j < kPPT; ++j) {
+        const int i = (int)threadIdx.x + j * kGemmThreads;
+        const int ph = i / (2 * kHead), kind = (i / kHead) & 1, pd = i % kHead;
+        const int pz = (int)((n0 + ph * kWF) / kHead) - which * p.heads;
+        const float* src = kind == 0 ? bias : gamma;
+        pv[j] = src != nullptr ? src[pz * kHead + pd] : 0.0f;
+    }
     f32x16 acc[kFI][kTJ];
     zero_acc(acc);
     if (t0 < g.rows) gemm_mainloop<T>(g, t0, n0, lds, acc);   // block-uniform (ends with a barrier)
-    float* prm = reinterpret_cast<float*>(lds + 4 * 64 * 256);   // [head][bias, gamma*sqrt(D)][128]
-    prm[(ph_ * 2 + 0) * kHead + pd_] = pbias;
-    prm[(ph_ * 2 + 1) * kHead + pd_] = pgam * p.rms_scale;
+    float* prm = reinterpret_cast<float*>(lds + kParamOff);
+#pragma unroll
+    for (int j = 0; j < kPPT; ++j) {
+        const int i = (int)threadIdx.x + j * kGemmThreads;
+        prm[i] = ((i / kHead) & 1) ? pv[j] * p.rms_scale : pv[j];
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
 
@@ -84,15 +108,15 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
     const int64_t extent = which == 0 ? p.mp : p.lp;
     T* __restrict__ out = static_cast<T*>(which == 0 ? p.qh : which == 1 ? p.k_out : p.vh);
     const bool trans = KT && which == 1;
-    uint8_t* region = lds + wave * (64 * 256);
+    uint8_t* region = lds + wave * kRegion;
     const float* pb = prm + (wf * 2 + 0) * kHead;
     const float* pg = prm + (wf * 2 + 1) * kHead;
 
-#pragma unroll 1
-    for (int half = 0; half < kTJ / 2; ++half) {
-#pragma unroll 1
-        for (int jj = 0; jj < 2; ++jj) {
-            const int tj = half * 2 + jj;
+#pragma unroll kGrpUnroll
+    for (int grp = 0; grp < kTJ / kJJ; ++grp) {
+#pragma unroll kGrpUnroll
+        for (int jj = 0; jj < kJJ; ++jj) {
+            const int tj = grp * kJJ + jj;
             // this token tile's accumulators (static register indices per case)
             float col[kFI][16];
             switch (tj) {
@@ -101,7 +125,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                 case 2: copy_col<(kTJ > 2 ? 2 : 0)>(acc, col); break;
                 default: copy_col<(kTJ > 2 ? 3 : 1)>(acc, col); break;
             }
-            const int tl = jj * 32 + fr;                      // staged row (token within the half)
+            const int tl = jj * 32 + fr;                      // staged row (token within the group)
             const int64_t t = t0 + wt * kWT + tj * 32 + fr;
             const int64_t tc = t < g.rows ? t : g.rows - 1;   // clamped for position reads
             const bool live = t < g.rows;
@@ -191,11 +215,11 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
             }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);      // the wave's LDS writes are done (its region is private)
-        const int64_t tw = t0 + wt * kWT + half * 64;   // first token of the staged rows
+        const int64_t tw = t0 + wt * kWT + grp * kStaged;   // first token of the staged rows
         if (!trans) {
             // token rows: 16 lanes per 256-byte row, 4 rows per instruction
 #pragma unroll 4
-            for (int it = 0; it < 64 / 4; ++it) {
+            for (int it = 0; it < kStaged / 4; ++it) {
                 const int row = it * 4 + (lane >> 4);
                 const int c = lane & 15;
                 const u32x4 w = *reinterpret_cast<const u32x4*>(region + row * 256 + ((c ^ stage_swz(row)) * 16));
@@ -204,11 +228,13 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
             }
         } else {
             // feature rows of the transposed k: lane (d, g) gathers feature d
-            // of tokens 8g .. 8g + 7 (eight 2-byte reads, one per token row)
+            // of tokens 8g .. 8g + 7 (eight 2-byte reads, one per token row);
+            // kG groups of 8 tokens, 64 / kG features per instruction
+            constexpr int kG = kStaged / 8;
 #pragma unroll 2
-            for (int it = 0; it < kHead / 8; ++it) {
-                const int d = it * 8 + (lane >> 3);
-                const int gg = lane & 7;
+            for (int it = 0; it < kHead * kG / 64; ++it) {
+                const int d = it * (64 / kG) + lane / kG;
+                const int gg = lane % kG;
                 const int off = (d & 7) * 2;
                 uint32_t wv[4];
 #pragma unroll
@@ -231,7 +257,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                 }
             }
         }
-        // the next half overwrites the staged rows: every lane's reads are done
+        // the next group overwrites the staged rows: every lane's reads are done
         __builtin_amdgcn_s_waitcnt(0xC07F);
     }
 }

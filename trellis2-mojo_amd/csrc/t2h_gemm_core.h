@@ -26,13 +26,14 @@
 // - 4 waves (2 x 2 of 128 x 128: 16 MFMA tiles, 256 accumulators per lane,
 //   one wave per SIMD); the stages are filled by direct-to-LDS loads
 //   (global_load_lds_dwordx4: a wave's 64 lanes fill one contiguous KB), the
-//   next stage's in flight while the current one's MFMAs run. The fused qkv
-//   kernel uses it: its epilogue needs the registers of one wave per SIMD.
+//   next stage's in flight while the current one's MFMAs run. It is kept as
+//   a build option (T2H_GEMM_WAVES / T2H_QKV_WAVES = 4).
 // - 8 waves (2 x 4 of 128 x 64: 8 MFMA tiles, 128 accumulators, two waves
 //   per SIMD); the next stage goes through registers: each wave writes it to
 //   LDS a slice per substep and refills the slice's registers with the stage
-//   after, and a wave raises its priority over its MFMAs. The linear and
-//   gated-residual kernels use it (2-5 % faster than the 4-wave form).
+//   after, and a wave raises its priority over its MFMAs. Every shipped
+//   kernel uses it: linear and gated residual 2-5 % faster than the 4-wave
+//   form, the fused qkv 10 %.
 // Tile numbers are dealt to the 8 XCDs in contiguous ranges and walked in
 // groups of a few token tiles, feature tile by feature tile, so the blocks
 // resident on one XCD share a few weight and token slabs in its L2.
