@@ -19,8 +19,9 @@ namespace {
 // ---- qkv linear + attention epilogue + head-major pack ----------------------
 // The qkv GEMM's output [rows, 3, H, 128] never reaches memory. A wave's 128
 // features are one head (q, k or v: head hg = n / 128, tensor hg / H, head
-// hg % H) for 128 tokens, and each token's head lives in two lanes (l and
-// l ^ 32, 64 values each). Per token, in the order of the separate kernels
+// hg % H) for kWT tokens (64 with 8 waves, 128 with 4), and each token's
+// head lives in two lanes (l and l ^ 32, 64 values each). Per token, in the
+// order of the separate kernels
 // (bias_rms_rope_qkv, pack_q_z, pack_kv_z): + bias; q/k: RMS over the head,
 // x * rsqrt(sum x^2) * (gamma * sqrt(D)); q/k: RoPE on the in-lane pairs
 // (2p, 2p + 1) with cos/sin from the phase table or from the token's
