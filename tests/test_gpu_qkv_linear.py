@@ -122,6 +122,29 @@ def test_pads_beyond_the_last_token_tile(dev):
     assert_close(vh, wv, torch.float16, "vh")
 
 
+@pytest.mark.parametrize("heads", [2, 4, 16])
+def test_other_head_counts(dev, heads):
+    """H = 2, 4 and 16: q, k and v start at feature tiles 0, H/2 and H, so
+    every wave finds its tensor and head from its feature tile (with H = 2
+    each tensor is one tile). Ragged rows (700), phase table, pads to 704."""
+    rows, k, mp = 700, 256, 704
+    n = 3 * heads * D
+    x = storage_round(orc.randn(5500 + heads, (rows, k)), torch.float16)
+    w = storage_round(orc.randn(5501 + heads, (n, k), std=0.05), torch.float16)
+    bias = orc.randn(5502 + heads, (n,), std=0.05)
+    gq = orc.randn(5503 + heads, (heads, D), mean=1.0, std=0.02)
+    gk = orc.randn(5504 + heads, (heads, D), mean=1.0, std=0.02)
+    phases = orc.rope_phases_from_positions(orc.grid_positions(16)[:rows], D, orc.rope_freqs(D))
+    wq, wk, wv = orc.attn_pack(orc.linear(x, w), heads, D, mp, mp, bias, gq, gk, phases)
+    qh, kt, vh = ops.qkv_linear_pack(to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16), heads,
+                                     bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev),
+                                     mp=mp, lp=mp, freqs=nn.rope_freqs(D), phases=to_dev(phases, dev))
+    assert qh.shape == (heads, mp, D) and kt.shape == (heads, D, mp) and vh.shape == (heads, mp, D)
+    assert_close(qh, wq, torch.float16, f"qh H={heads}")
+    assert_close(kt, wk, torch.float16, f"kt H={heads}")
+    assert_close(vh, wv, torch.float16, f"vh H={heads}")
+
+
 def test_zero_rows_and_errors(dev):
     w = torch.zeros((3 * H * D, C), dtype=torch.float16, device=dev)
     qh, kt, vh = ops.qkv_linear_pack(torch.zeros((0, C), dtype=torch.float16, device=dev), w, H, mp=64, lp=64,
