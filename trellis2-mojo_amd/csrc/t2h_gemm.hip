@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                 const int c = lane & 15;
                 const u32x4 w = *reinterpret_cast<const u32x4*>(region + row * 256 + ((c ^ stage_swz(row)) * 16));
                 const int64_t t = tw + row;
-                if (t < extent) *reinterpret_cast<u32x4*>(out + ((int64_t)z * extent + t) * kHead + c * 8) = w;
+                if (t < extent) out_store16(out + ((int64_t)z * extent + t) * kHead + c * 8, w);
             }
         } else {
             // feature rows of the transposed k: lane (d, g) gathers feature d
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                     w.y = wv[1];
                     w.z = wv[2];
                     w.w = wv[3];
-                    *reinterpret_cast<u32x4*>(out + ((int64_t)z * kHead + d) * p.lp + t) = w;
+                    out_store16(out + ((int64_t)z * kHead + d) * p.lp + t, w);
                 }
             }
         }

@@ -495,6 +495,16 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& a, int64_t t0, int
     }
 }
 
+#ifndef T2H_GEMM_NTS
+#define T2H_GEMM_NTS 1
+#endif
+// A 16-byte store of an epilogue; non-temporal with T2H_GEMM_NTS (the GEMM
+// never re-reads its outputs, so they need not displace operands in L2).
+__device__ __forceinline__ void out_store16(void* p, u32x4 w) {
+    if constexpr (T2H_GEMM_NTS) __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+    else *reinterpret_cast<u32x4*>(p) = w;
+}
+
 __device__ __forceinline__ void zero_acc(f32x16 (&acc)[kFI][kTJ]) {
 #pragma unroll
     for (int fi = 0; fi < kFI; ++fi)

@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
             const int c = fr;
             const int64_t t = t0 + r;
             const u32x4 w = *reinterpret_cast<const u32x4*>(lds + r * (kBF * 2) + ((c ^ (r & 31)) * 16));
-            if (t < a.rows) *reinterpret_cast<u32x4*>(out + t * a.ldo + n0 + c * 8) = w;
+            if (t < a.rows) out_store16(out + t * a.ldo + n0 + c * 8, w);
         }
     } else {
 #pragma unroll
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_kernel(GemmAr
                     float v[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) v[i] = epi_f<ACT>(acc[fi][tj][q * 4 + i], bv[q][i]);
-                    store_elems<O, 4>(out + t * a.ldo + n, v);
+                    store_elems<O, 4, T2H_GEMM_NTS>(out + t * a.ldo + n, v);
                 }
             }
         }
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(Ge
             const int c = fr;
             const int64_t t = t0 + r;
             const u32x4 w = *reinterpret_cast<const u32x4*>(lds + r * (kBF * 2) + ((c ^ (r & 31)) * 16));
-            if (t < a.rows) *reinterpret_cast<u32x4*>(out + t * a.ldo + n0 + c * 8) = w;
+            if (t < a.rows) out_store16(out + t * a.ldo + n0 + c * 8, w);
         }
     } else {
         // per feature group: its residual values and parameters are all
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void gemm_res_kernel(Ge
                 for (int q = 0; q < 4; ++q) {
                     float u[4];
                     join4(fi, tj, q, bv[q], gv[q], rv[tj][q], u);
-                    store_elems<O, 4>(out + t * a.ldo + n0 + wf * kWF + fi * 32 + q * 8 + h * 4, u);
+                    store_elems<O, 4, T2H_GEMM_NTS>(out + t * a.ldo + n0 + wf * kWF + fi * 32 + q * 8 + h * 4, u);
                 }
             }
         }
