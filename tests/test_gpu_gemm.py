@@ -71,6 +71,26 @@ def test_more_tiles_than_cus_bit_exact(dev, out_dtype, act):
     assert np.array_equal(host(out), want)
 
 
+def test_long_k_tile_order_bit_exact(dev):
+    """K = 4096 (64 k steps; the tile order groups 2 token tiles instead of
+    4) with 3 token tiles, the last ragged: a group of 2 and a remainder of
+    1. Operands in {-1, 0, 1}: exact sums, |sums| < 2048, so both the f32
+    and the f16 output equal the oracle bit for bit, as does the gated
+    residual join on the same GEMM."""
+    rng = np.random.default_rng(29)
+    m, n, k = 600, 512, 4096
+    a = rng.integers(-1, 2, (m, k)).astype(np.float32)
+    w = rng.integers(-1, 2, (n, k)).astype(np.float32)
+    want = orc.linear(a, w)
+    assert np.abs(want).max() < 2048
+    ad, wd = to_dev(a, dev, torch.float16), to_dev(w, dev, torch.float16)
+    assert np.array_equal(host(ops.linear(ad, wd, out_dtype=torch.float32)), want)
+    assert np.array_equal(host(ops.linear(ad, wd)), want)
+    res = rng.integers(-8, 9, (m, n)).astype(np.float32)
+    got = ops.linear_gate_residual(ad, wd, to_dev(res, dev, torch.float32))
+    assert np.array_equal(host(got), orc.gate_residual(res, want, None, None, None))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [1, 129, 1000])
 def test_random_operands_within_sum_bound(dev, dtype, m):

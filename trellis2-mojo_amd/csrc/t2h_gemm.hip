@@ -282,6 +282,7 @@ hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, 
     if (p.lp > span) span = p.lp;
     g.ftiles = g.n / kBF;
     g.nblocks = ((span + kBT - 1) / kBT) * g.ftiles;
+    g.tgroup = tile_group(g.k);
     if (g.nblocks == 0) return hipSuccess;
     if (g.dtype == T2H_F16) return qkv_typed<_Float16>(g, p, tab, s);
     return qkv_typed<__bf16>(g, p, tab, s);

@@ -270,6 +270,7 @@ int32_t gemm_k_step() { return kBK; }
 hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
     a.ftiles = a.n / kBF;
     a.nblocks = ((a.rows + kBT - 1) / kBT) * a.ftiles;
+    a.tgroup = tile_group(a.k);
     if (a.nblocks == 0) return hipSuccess;
     if (a.dtype == T2H_F16) return gemm_typed<_Float16>(a, s);
     return gemm_typed<__bf16>(a, s);
@@ -278,6 +279,7 @@ hipError_t launch_gemm(GemmArgs a, hipStream_t s) {
 hipError_t launch_gemm_residual(GemmArgs a, hipStream_t s) {
     a.ftiles = a.n / kBF;
     a.nblocks = ((a.rows + kBT - 1) / kBT) * a.ftiles;
+    a.tgroup = tile_group(a.k);
     if (a.nblocks == 0) return hipSuccess;
     if (a.dtype == T2H_F16) return gemm_res_typed<_Float16>(a, s);
     return gemm_res_typed<__bf16>(a, s);

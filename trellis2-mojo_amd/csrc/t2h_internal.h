@@ -120,6 +120,7 @@ struct GemmArgs {
     int32_t out_dtype;       // T2H_F32 or dtype
     int64_t nblocks;         // set by the launcher: token tiles x feature tiles
     int32_t ftiles;          // feature tiles
+    int32_t tgroup;          // set by the launcher: token tiles per group of the tile order
     // residual epilogue (t2h_linear_gate_residual): out = res + fl(fl(acc + bias) * gate[b])
     const void* res;         // [rows, n], rows ldo elements apart, out_dtype; may alias out
     const float* gate;       // gate rows [nbatch, n] gate_stride apart, or nullptr (ungated)
