@@ -178,8 +178,11 @@ int orc_binop_rows(const float* x, const float* other, const int64_t* row_map,
     return 0;
 }
 
-void orc_binop_scalar(const float* x, float v, float* out, int64_t n, int op) {
-    for (int64_t i = 0; i < n; ++i) out[i] = apply_op(x[i], v, op);
+void orc_binop_scalar(const float* x, float v, float* out, int64_t n, int op, int reverse) {
+    /* _opscalar_span (sparse/tensor.mojo:469-524): x OP v, or v OP x when
+     * reverse (only SUB and DIV have a reverse form; ADD and MUL ignore it) */
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = (reverse && (op == 1 || op == 3)) ? apply_op(v, x[i], op) : apply_op(x[i], v, op);
 }
 
 void orc_binop_flat(const float* x, const float* y, float* out, int64_t n, int op) {

@@ -61,8 +61,8 @@ void orc_batch_broadcast_map(const int64_t* offsets, int64_t batch_size,
  * op: 0 add, 1 sub, 2 mul, 3 div (sparse/tensor.mojo:4-7). */
 int orc_binop_rows(const float* x, const float* other, const int64_t* row_map,
                    float* out, int64_t rows, int64_t c, int64_t other_c, int op);
-/* Tensor._binop_scalar(v, op): x OP v elementwise */
-void orc_binop_scalar(const float* x, float v, float* out, int64_t n, int op);
+/* Tensor._binop_scalar(v, op, reverse): x OP v elementwise, v OP x when reverse */
+void orc_binop_scalar(const float* x, float v, float* out, int64_t n, int op, int reverse);
 /* Tensor._binop_flat: x OP y elementwise (sparse/tensor.mojo:193-198) */
 void orc_binop_flat(const float* x, const float* y, float* out, int64_t n, int op);
 

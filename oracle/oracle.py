@@ -166,10 +166,12 @@ def binop_rows(x, other, row_map, op: int) -> np.ndarray:
     return out
 
 
-def binop_scalar(x, v: float, op: int) -> np.ndarray:
+def binop_scalar(x, v: float, op: int, reverse: bool = False) -> np.ndarray:
+    """Tensor._binop_scalar (sparse/tensor.mojo:200-203): x OP v, or v OP x
+    when reverse."""
     x = _f32(x)
     out = np.empty_like(x)
-    lib().orc_binop_scalar(_p(x), ctypes.c_float(v), _p(out), _i64(x.size), op)
+    lib().orc_binop_scalar(_p(x), ctypes.c_float(v), _p(out), _i64(x.size), op, int(reverse))
     return out
 
 

@@ -189,6 +189,65 @@ def test_fused_gated_join_affine_multibatch(dev, dtype):
     assert_close(yo, orc.layernorm(xw, 1e-6, True, w, b), dtype, f"gated join + affine LN {dtype}")
 
 
+@pytest.mark.parametrize("in_place", [False, True])
+@pytest.mark.parametrize("cols", [1, 100, 1000, 1280, 1536, 1537])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_fused_join_generic_widths(dev, dtype, cols, in_place):
+    """The fused join + LN at widths off the one-wave-per-row fast path (all
+    but 1536; f32 1280 is 5 vectors per lane, which has no fast variant),
+    with x_out a separate tensor or x itself (x_out may alias x). The stored
+    residual must equal the oracle's rounded once, and the LN must read it,
+    not x + gate*h recomputed over an already updated x."""
+    rows = 37
+    x = storage_round(orc.randn(3000 + cols, (rows, cols)), dtype)
+    h = storage_round(orc.randn(3001, (rows, cols)), dtype)
+    bias = orc.randn(3002, (cols,), std=0.05)
+    gate = orc.randn(3003, (cols,), std=0.5)
+    shift = orc.randn(3004, (cols,), std=0.1)
+    scale = orc.randn(3005, (cols,), std=0.1)
+    dx, dh = to_dev(x, dev, dtype), to_dev(h, dev, dtype)
+    db, dg, ds, dc = (to_dev(a, dev) for a in (bias, gate, shift, scale))
+    xo, yo = ops.gate_residual_ln_modulate(dx, dh, gate=dg, bias=db, eps=1e-6, shift=ds, scale=dc,
+                                           x_out=dx if in_place else None)
+    assert (xo.data_ptr() == dx.data_ptr()) == in_place
+    xw = storage_round(orc.gate_residual(x, h, gate, bias=bias), dtype)
+    assert bits_equal(xo, xw, dtype), f"joined residual, cols {cols}"
+    assert_close(yo, orc.ln_modulate(xw, shift, scale, eps=1e-6), dtype, f"join LN+mod cols {cols} in_place {in_place}")
+
+
+@pytest.mark.parametrize("cols", [100, 1000, 1280, 1536])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_block_join_ln_generic_widths(dev, dtype, cols):
+    """t2h_block_join_ln always updates x in place (gpu/block.mojo:324-349,
+    356-381): gated join + modulated norm and ungated join + affine norm over
+    the 12*C const buffer, at fast and generic widths."""
+    from t2h import block
+
+    rows = 29
+    x = storage_round(orc.randn(3100, (rows, cols)), dtype)
+    h = storage_round(orc.randn(3101, (rows, cols)), dtype)
+    m = [orc.randn(3102 + i, (1, cols), std=0.1) for i in range(6)]
+    w2 = orc.randn(3108, (cols,), mean=1.0, std=0.1)
+    b2 = orc.randn(3109, (cols,), std=0.05)
+    biases = [orc.randn(3110 + i, (cols,), std=0.02) for i in range(3)]
+    bk = block.pack_block_consts([to_dev(mm, dev) for mm in m], to_dev(w2, dev), to_dev(b2, dev),
+                                 *[to_dev(b, dev) for b in biases])
+    v = lambda k: host(bk)[k * cols:(k + 1) * cols]
+    # self join (bias 2C, gate 3C) + norm2 affine (4C, 5C)
+    dx = to_dev(x, dev, dtype)
+    dst = torch.empty_like(dx)
+    ops.block_join_ln(dx, to_dev(h, dev, dtype), dst, bk, 2 * cols, 1, 4 * cols, 2)
+    xw = storage_round(orc.gate_residual(x, h, v(3), bias=v(2)), dtype)
+    assert bits_equal(dx, xw, dtype), f"gated join cols {cols}"
+    assert_close(dst, orc.layernorm(xw, 1e-6, True, v(4), v(5)), dtype, f"join + affine LN cols {cols}")
+    # cross join (bias 6C, ungated) + norm3 modulate (8C, 9C)
+    dx = to_dev(x, dev, dtype)
+    ops.block_join_ln(dx, to_dev(h, dev, dtype), dst, bk, 6 * cols, 0, 8 * cols, 1)
+    xw = storage_round(orc.gate_residual(x, h, None, bias=v(6)), dtype)
+    assert bits_equal(dx, xw, dtype), f"ungated join cols {cols}"
+    assert_close(dst, orc.ln_modulate(xw, v(8), v(9), eps=1e-6), dtype, f"join + LN mod cols {cols}")
+
+
 def test_modulation_chunk_views(dev):
     """Modulation.chunks (share_mod) -> six strided [B, C] views read in place."""
     b, c = 2, 1536

@@ -137,6 +137,23 @@ def test_empty_rows_zero_pads(dev):
         assert t.numel() == h * 64 * d and not t.any()
 
 
+@pytest.mark.parametrize("k_transposed", [True, False])
+def test_empty_rows_with_rope_sources(dev, k_transposed):
+    """rows = 0 with RoPE on and a non-NULL coords pointer (a zero-row view of
+    a larger coords tensor) or a phase table: no coordinate, phase or row is
+    read, and every output row is a zero pad."""
+    h, d = 4, 128
+    qkv = torch.empty((0, 3 * h * d), device=dev)
+    q, k, v = _views(qkv, h, d)
+    coords = torch.zeros((16, 4), dtype=torch.int32, device=dev)[:0]
+    assert coords.data_ptr() != 0 and coords.is_contiguous()
+    phases = torch.ones((1, d // 2, 2), device=dev)
+    for src in (dict(coords=coords), dict(phases=phases)):
+        qh, ko, vh = ops.attn_pack(q, k, v, mp=64, lp=64, freqs=nn.rope_freqs(d), k_transposed=k_transposed, **src)
+        for t in (qh, ko, vh):
+            assert t.numel() == h * 64 * d and not t.any()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_many_heads_and_table_phases(dev, dtype):
     """20 heads x 64 (beyond the one-wave-per-row kernel's 16) with a phase

@@ -100,6 +100,67 @@ def test_gate_and_residual_exact_f32():
     assert np.array_equal(orc.gate_residual(x.reshape(-1, 32), h.reshape(-1, 32), g, offsets=off, bias=b), want)
 
 
+_NP_OPS = {orc.OP_ADD: np.add, orc.OP_SUB: np.subtract, orc.OP_MUL: np.multiply, orc.OP_DIV: np.divide}
+
+
+def test_binop_rows_every_op_exact_f32():
+    """Tensor._binop_rows (sparse/tensor.mojo:205-219) for all four ops, with
+    [B, C] rows and per-batch scalars [B, 1], over offsets with an empty
+    batch: self OP other[row_map[r]] is one IEEE f32 op per element, so numpy
+    float32 gives the same bits. The swapped operand order (other OP self) of
+    SUB and DIV, and a row map shifted by one batch, both fail the check."""
+    x = orc.randn(2000, (37, 24))
+    other = orc.randn(2001, (3, 24), mean=1.5)     # away from 0 for DIV
+    offsets = np.array([0, 10, 10, 37], np.int64)   # batch 1 is empty
+    rm = orc.batch_broadcast_map(offsets)
+    assert rm.tolist() == [0] * 10 + [2] * 27
+    for op, f in _NP_OPS.items():
+        assert np.array_equal(orc.binop_rows(x, other, rm, op), f(x, other[rm])), op
+        s = other[:, :1].copy()
+        assert np.array_equal(orc.binop_rows(x, s, rm, op), f(x, s[rm])), op
+    for op in (orc.OP_SUB, orc.OP_DIV):
+        got = orc.binop_rows(x, other, rm, op)
+        assert not np.array_equal(got, _NP_OPS[op](other[rm], x))            # swapped operands
+        assert not np.array_equal(got, _NP_OPS[op](x, other[np.maximum(rm - 1, 0)]))   # shifted map
+    with pytest.raises(ValueError, match="incompatible row size"):
+        orc.binop_rows(x, other[:, :5], rm, orc.OP_ADD)
+
+
+def test_binop_flat_and_scalar_every_op_exact_f32():
+    """_binop_flat (sparse/tensor.mojo:193-198) and _binop_scalar with its
+    reverse form (200-203, _opscalar_span 469-524): x OP v, or v OP x for
+    reverse SUB/DIV; reverse ADD/MUL equal the forward form (commutative).
+    The forward result of SUB/DIV differs from the reverse one, so an
+    operand swap in either form fails."""
+    x = orc.randn(2002, (5, 131))       # 655 elements: SIMD body and scalar tail
+    y = orc.randn(2003, (5, 131), mean=-2.0)
+    v = np.float32(0.37)
+    for op, f in _NP_OPS.items():
+        assert np.array_equal(orc.binop_flat(x, y, op), f(x, y)), op
+        assert np.array_equal(orc.binop_scalar(x, float(v), op), f(x, v)), op
+        rev = orc.binop_scalar(x, float(v), op, reverse=True)
+        assert np.array_equal(rev, f(v, x) if op in (orc.OP_SUB, orc.OP_DIV) else f(x, v)), op
+    for op in (orc.OP_SUB, orc.OP_DIV):
+        assert not np.array_equal(orc.binop_flat(x, y, op), _NP_OPS[op](y, x))
+        assert not np.array_equal(orc.binop_scalar(x, float(v), op), _NP_OPS[op](v, x))
+    with pytest.raises(ValueError, match="size mismatch"):
+        orc.binop_flat(x, y[:, :3], orc.OP_ADD)
+
+
+def test_modulation_add_exact_f32():
+    """Modulation.chunks, share_mod branch (sparse/transformer/modulated.mojo:
+    41-48): m[r, j] = mod[r, j] + modulation[j], one f32 add, broadcast over
+    rows. Adding only the first C-wide chunk of modulation to all six chunks,
+    or pairing row r of mod with a row-offset slice, fails the check."""
+    c = 48
+    mod = orc.randn(2004, (3, 6 * c))
+    modulation = orc.randn(2005, (6 * c,), std=0.5)
+    got = orc.modulation_add(mod, modulation)
+    assert np.array_equal(got, mod + modulation[None, :])
+    assert not np.array_equal(got, mod + np.tile(modulation[:c], 6)[None, :])
+    assert not np.array_equal(got, mod + np.roll(modulation, c)[None, :])
+
+
 # ---- LayerNorm: float64 closed form ---------------------------------------------
 def _ln64(x, eps, w=None, b=None):
     x = x.astype(np.float64)
@@ -454,6 +515,61 @@ def test_flow_schedule_and_sampler_float64():
     for a, b in zip(ts, ts[1:]):
         want = want * (1.0 + (a - b))
     assert np.max(np.abs(out - want) / np.abs(want)) < 1e-5 and len(xs) == 12 and len(x0s) == 12
+
+
+class _StubModel:
+    """A velocity model that returns a distinct constant for each branch
+    (2 for the positive condition, -3 for the negative one) and records its
+    calls as (t1000, use_neg)."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, x_t, t1000, use_neg):
+        self.calls.append((t1000, use_neg))
+        return np.full_like(x_t, -3.0 if use_neg else 2.0)
+
+
+def _infer(mode, g, t, lo=0.3, hi=0.6, gr=0.0):
+    m = _StubModel()
+    x = orc.randn(2100, (4, 16))
+    out = orc.flow_inference(m, x, t, mode, g, lo, hi, gr, 1e-5, None)
+    return out, m.calls, x
+
+
+def test_flow_inference_branches():
+    """_inference (samplers/flow_euler.mojo:151-181) with a stub model:
+    - no guidance, g == 1 and g == 0 each make one call and return that
+      branch unchanged, also with guidance_rescale > 0 (rescale is skipped);
+    - CFG returns fl(g*pos) + fl((1-g)*neg) from pos then neg;
+    - CFG_INTERVAL applies CFG on the closed interval [lo, hi] (t exactly
+      on lo and on hi included) and the positive branch outside it, while
+      plain CFG ignores the interval;
+    - guidance_rescale > 0 routes the CFG prediction through _rescale_pred;
+    - the model sees t * 1000 in float64."""
+    pos = np.float32(2.0)
+    neg = np.float32(-3.0)
+    out, calls, _ = _infer(orc.GUIDANCE_NONE, 3.0, 0.45)
+    assert calls == [(1000.0 * 0.45, False)] and np.all(out == pos)
+    out, calls, _ = _infer(orc.GUIDANCE_CFG, 1.0, 0.45, gr=0.7)
+    assert calls == [(1000.0 * 0.45, False)] and np.all(out == pos)
+    out, calls, _ = _infer(orc.GUIDANCE_CFG, 0.0, 0.45, gr=0.7)
+    assert calls == [(1000.0 * 0.45, True)] and np.all(out == neg)
+    g = 3.0
+    cfg = pos * np.float32(g) + neg * np.float32(1.0 - g)
+    assert cfg == np.float32(12.0)
+    out, calls, _ = _infer(orc.GUIDANCE_CFG, g, 0.9)              # outside [lo, hi]: plain CFG ignores it
+    assert [c[1] for c in calls] == [False, True] and np.all(out == cfg)
+    for t in (0.3, 0.45, 0.6):                                     # inclusive ends
+        out, calls, _ = _infer(orc.GUIDANCE_CFG_INTERVAL, g, t)
+        assert [c[1] for c in calls] == [False, True] and np.all(out == cfg), t
+    for t in (0.29999, 0.60001, 1.0):
+        out, calls, _ = _infer(orc.GUIDANCE_CFG_INTERVAL, g, t)
+        assert calls == [(1000.0 * t, False)] and np.all(out == pos), t
+    out, calls, x = _infer(orc.GUIDANCE_CFG_INTERVAL, g, 0.6, gr=0.7)
+    assert len(calls) == 2
+    assert not np.array_equal(out, np.full_like(x, cfg))
+    assert np.array_equal(out, orc.flow_rescale(x, np.full_like(x, cfg), np.full_like(x, pos), 0.6, 1e-5, 0.7))
 
 
 # ---- weight GEMM: gpu/linear.mojo:108-160, 326-388 ---------------------------

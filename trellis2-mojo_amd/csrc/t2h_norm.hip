@@ -62,9 +62,9 @@ __global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
     const int64_t r = r0 + wave;
     const bool live = r < a.rows;
     const int64_t rl = live ? r : a.rows - 1;   // dead waves load a valid row, store nothing
-    const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* x = static_cast<const T*>(a.x);   // may alias x_out: no __restrict__
     const T* __restrict__ h = static_cast<const T*>(a.h);
-    T* __restrict__ xo = static_cast<T*>(a.x_out);
+    T* xo = static_cast<T*>(a.x_out);
     T* __restrict__ yo = static_cast<T*>(a.y_out);
     const int64_t base = rl * (int64_t)C;
 
@@ -176,13 +176,16 @@ __global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
 }
 
 // Any cols: one 256-thread block per row (grid-stride), block reduction
-// through LDS, values re-read from memory for each pass.
+// through LDS, values re-read from memory for each pass. With JOIN, pass 1
+// writes x_out and passes 2 and 3 read the stored (already rounded) value
+// back: x_out may alias x, so recomputing x + gate*h from x would add the
+// gated term twice. Each thread reads back only the elements it wrote.
 template <typename T, bool JOIN>
 __global__ __launch_bounds__(kBlock) void ln_rows_generic(LnArgs a) {
     __shared__ float red[kWavesPerBlock];
-    const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* x = static_cast<const T*>(a.x);   // may alias x_out: no __restrict__
     const T* __restrict__ h = static_cast<const T*>(a.h);
-    T* __restrict__ xo = static_cast<T*>(a.x_out);
+    T* xo = static_cast<T*>(a.x_out);
     T* __restrict__ yo = static_cast<T*>(a.y_out);
     const BatchMap bm{a.batch.offsets, a.batch.rows_per_batch, a.batch.nbatch};
     const int C = a.cols;
@@ -199,7 +202,7 @@ __global__ __launch_bounds__(kBlock) void ln_rows_generic(LnArgs a) {
     for (int64_t r = blockIdx.x; r < a.rows; r += gridDim.x) {
         const int64_t base = r * (int64_t)C;
         const int32_t b = (a.mode == T2H_LN_MODULATE || (JOIN && a.gate)) ? bm.batch_of(r) : 0;
-        auto value = [&](int c) -> float {
+        auto joined = [&](int c) -> float {   // pass 1: x + fl(fl(h + bias) * gate), rounded to T
             float xv = ld1(x + base + c);
             if (JOIN) {
                 float t = ld1(h + base + c);
@@ -209,9 +212,12 @@ __global__ __launch_bounds__(kBlock) void ln_rows_generic(LnArgs a) {
             }
             return xv;
         };
+        auto value = [&](int c) -> float {    // passes 2 and 3: the row as pass 1 left it
+            return JOIN ? ld1(xo + base + c) : ld1(x + base + c);
+        };
         float s = 0.0f;
         for (int c = tid; c < C; c += kBlock) {
-            const float xv = value(c);
+            const float xv = joined(c);
             if (JOIN) st1(xo + base + c, xv);
             s += xv;
         }

@@ -104,7 +104,8 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
     T* __restrict__ out = static_cast<T*>(which == 0 ? a.qh : which == 1 ? a.k_out : a.vh);
     const float* __restrict__ bias = which == 0 ? a.bias_q : which == 1 ? a.bias_k : a.bias_v;
     const float* __restrict__ gamma = which == 0 ? a.gamma_q : which == 1 ? a.gamma_k : nullptr;
-    const bool rope = a.use_rope && which < 2;
+    // with no token rows every output is a pad: no phase (coords) or row read
+    const bool rope = a.use_rope && which < 2 && a.rows > 0;
 
     // this lane's token rows (clamped for the loads; rows >= a.rows are pads)
     int64_t rl[kPackIters];
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
 #pragma unroll
             for (int it = 0; it < kPackIters; ++it) {
                 float pos[T2H_MAX_POS_DIM];
-                src.get(a.rows > 0 ? rl[it] : 0, pos);
+                src.get(rl[it], pos);
 #pragma unroll
                 for (int j = 0; j < P; ++j) slot_phase(pos, ax[j], fr[j], pc[it][j], ps[it][j]);
             }
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     T* __restrict__ out = static_cast<T*>(which == 0 ? a.qh : which == 1 ? a.k_out : a.vh);
     const float* __restrict__ bias = which == 0 ? a.bias_q : which == 1 ? a.bias_k : a.bias_v;
     const float* __restrict__ gamma = which == 0 ? a.gamma_q : which == 1 ? a.gamma_k : nullptr;
-    const bool rope = a.use_rope && which < 2;
+    const bool rope = a.use_rope && which < 2 && a.rows > 0;   // no rows: all pads
 
     const int my_slot = lane % HALF;
     const int my_axis = tab.axis[my_slot];
