@@ -118,6 +118,8 @@ class Chain:
             return lambda: self.torch.mul(self.u, 1.0, out=self.gout)
         if name == "chain":
             return self.step
+        if name in self.NEXT_OPS:
+            return self.next_op(name)
         if name in self.GEMM_OPS:
             g = self.gemm_state()
             if name == "linear_qkv":
@@ -131,6 +133,69 @@ class Chain:
                                              gamma_k=self.gk, mp=g["mp"], lp=g["mp"], freqs=self.freqs,
                                              phases=g["phases"], k_transposed=True)
         raise KeyError(name)
+
+    # the per-token work around the chain on the config-5 rows (f16): the
+    # block glue over one const buffer (chains stubbed by a resident tensor,
+    # so only the glue kernels run), the attention epilogue + head-major pack,
+    # and the sampler step on the tokens' 32-channel f32 latent
+    NEXT_OPS = ("block_glue_fused", "block_glue_unfused", "attn_pack_kt", "attn_pack_krows",
+                "flow_euler_step_cfg", "flow_euler_step_cfg_rescale")
+
+    def next_state(self):
+        if getattr(self, "_next", None) is None:
+            torch = self.torch
+            from t2h import block, ops
+
+            T, C, H = self.T, self.C, self.H
+            dev = self.x.device
+            m = [self.shift, self.scale, self.gate, self.shift, self.scale, self.gate]
+            ones = torch.ones(C, dtype=torch.float32, device=dev)
+            st = {"bk": block.pack_block_consts(m, ones, self.shift.reshape(-1), self.bias[:C], self.bias[C:2 * C],
+                                                self.bias[2 * C:3 * C]),
+                  "xs": self.x.clone(), "mp": (T + 63) // 64 * 64}
+            st["q3"] = self.u[:, :3 * C].contiguous().reshape(T, 3, H, self.D)
+            st["b3"] = self.bias[:3 * C].reshape(3, H * self.D)
+            g = torch.Generator(device=dev).manual_seed(7)
+            st["lat"] = [torch.randn((T, 32), generator=g, device=dev) for _ in range(3)]
+            st["lat_out"] = [torch.empty((T, 32), device=dev) for _ in range(2)]
+            st["ws"] = torch.empty(ops.flow_euler_workspace(T, 32, 2), dtype=torch.uint8, device=dev)
+            self._next = st
+        return self._next
+
+    def next_bytes(self, name):
+        T, C = self.T, self.C
+        e = 2
+        n = T * 32 * 4
+        mp = (T + 63) // 64 * 64
+        return {"block_glue_fused": 13 * T * C * e, "block_glue_unfused": 15 * T * C * e,   # row-passes of C
+                "attn_pack_kt": T * 3 * C * e + 3 * mp * C * e + T * 16,
+                "attn_pack_krows": T * 3 * C * e + 3 * mp * C * e + T * 16,
+                # CFG: reads x, v_pos, v_neg, writes x_prev, pred_x0; the rescale's
+                # statistics pass reads the three inputs once more
+                "flow_euler_step_cfg": 5 * n, "flow_euler_step_cfg_rescale": 8 * n}[name]
+
+    def next_op(self, name):
+        from t2h import block, ops
+
+        st = self.next_state()
+        if name.startswith("block_glue"):
+            stub = lambda h: self.y
+            fused = name.endswith("_fused")
+            return lambda: block.cross_block_enqueue(st["xs"], st["bk"], stub, stub, stub, fused=fused)
+        if name.startswith("attn_pack"):
+            q3, b3, mp = st["q3"], st["b3"], st["mp"]
+            kt = name == "attn_pack_kt"
+            return lambda: ops.attn_pack(q3[:, 0], q3[:, 1], q3[:, 2], mp=mp, lp=mp, bias_q=b3[0], bias_k=b3[1],
+                                         bias_v=b3[2], gamma_q=self.gq, gamma_k=self.gk, freqs=self.freqs,
+                                         coords=self.coords, k_transposed=kt)
+        lat, lo = st["lat"], st["lat_out"]
+        if name == "flow_euler_step_cfg":
+            return lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2], guidance_strength=3.0,
+                                               x_prev=lo[0], pred_x0=True)
+        # CFG 3.0 + rescale 0.5 over one token segment
+        return lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2], guidance_strength=3.0,
+                                           guidance_rescale=0.5, seg_offsets=[0, self.T], workspace=st["ws"],
+                                           x_prev=lo[0])
 
     # the GEMM rows (f16 operands on the matrix cores): flops per launch
     GEMM_OPS = ("linear_qkv", "linear_fc1_gelu", "qkv_linear_pack", "linear_fc2_gate_residual")
@@ -308,42 +373,10 @@ def next_rows(torch, dev, chain, reps):
                      "pct_of_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 2)}
         log(f"  {name:<26s} {ms*1e3:8.1f} us  {nbytes/ms/1e6:8.1f} GB/s ({nbytes/ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
 
-    m = [chain.shift, chain.scale, chain.gate, chain.shift, chain.scale, chain.gate]
-    ones = torch.ones(C, dtype=torch.float32, device=dev)
-    bk = block.pack_block_consts(m, ones, chain.shift.reshape(-1), chain.bias[:C], chain.bias[C:2 * C],
-                                 chain.bias[2 * C:3 * C])
-    xs = chain.x.clone()
-    hres = chain.y
-    stub = lambda h: hres
-    for fused, nrows in ((True, 13), (False, 15)):   # row-passes of C elements per block
-        rec(f"block_glue_{'fused' if fused else 'unfused'}",
-            lambda f=fused: block.cross_block_enqueue(xs, bk, stub, stub, stub, fused=f), nrows * T * C * e)
-    del xs
+    for name in Chain.NEXT_OPS:
+        rec(name, chain.op(name), chain.next_bytes(name))
+    chain._next = None
     mp = (T + 63) // 64 * 64
-    qkv = chain.u[:, :3 * C].contiguous()
-    q3 = qkv.reshape(T, 3, H, D)
-    b3 = chain.bias[:3 * C].reshape(3, H * D)
-    for kt in (True, False):   # k as the reference's [H, D, lp], or row-major [H, lp, D]
-        rec(f"attn_pack_k{'t' if kt else 'rows'}",
-            lambda kt=kt: ops.attn_pack(q3[:, 0], q3[:, 1], q3[:, 2], mp=mp, lp=mp, bias_q=b3[0], bias_k=b3[1],
-                                        bias_v=b3[2], gamma_q=chain.gq, gamma_k=chain.gk, freqs=chain.freqs,
-                                        coords=chain.coords, k_transposed=kt),
-            T * 3 * C * e + 3 * mp * C * e + T * 16)
-    del qkv, q3
-    # sampler step on the config-5 tokens' 32-channel latent (f32, as the
-    # reference's sampler state), CFG 3.0 + rescale 0.5 over one segment:
-    # statistics pass reads x, v_pos, v_neg; the update pass reads them again
-    # and writes x_prev and pred_x0
-    g = torch.Generator(device=dev).manual_seed(7)
-    lat = [torch.randn((T, 32), generator=g, device=dev) for _ in range(3)]
-    ws = torch.empty(ops.flow_euler_workspace(T, 32, 2), dtype=torch.uint8, device=dev)
-    n = T * 32 * 4
-    rec("flow_euler_step_cfg", lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2],
-                                                           guidance_strength=3.0), 5 * n)
-    rec("flow_euler_step_cfg_rescale", lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2],
-                                                                   guidance_strength=3.0, guidance_rescale=0.5,
-                                                                   seg_offsets=[0, T], workspace=ws), 8 * n)
-    del lat, ws
     # N2's GEMM half on the matrix cores (f16 operands, f32 sums), config-5
     # tokens: the qkv linear alone, the MLP's first linear with GELU-tanh in
     # its store, and the qkv linear fused with the attention epilogue and the
@@ -430,7 +463,8 @@ def main():
             tf = chain.gemm_flops(args.op) / (ms / args.steps) / 1e9
             log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {tf:.1f} TFLOP/s")
             return
-        nb = chain.chain_bytes if args.op == "chain" else chain.bytes[args.op]
+        nb = chain.chain_bytes if args.op == "chain" else (
+            chain.next_bytes(args.op) if args.op in chain.NEXT_OPS else chain.bytes[args.op])
         log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {nb/(ms/args.steps)/1e6:.1f} GB/s")
         return
 

@@ -91,9 +91,9 @@ def test_config5_rope_keeps_pair_norms(chain):
     from t2h import ops
 
     T, H, D = chain.T, chain.H, chain.D
-    for src, out in ((chain.q, chain.qo), (chain.k, chain.ko)):
+    for src, gamma, out in ((chain.q, chain.gq, chain.qo), (chain.k, chain.gk, chain.ko)):
         rms = torch.empty_like(src)
-        ops.qk_rmsnorm_rope(q=src, gamma_q=chain.gq, use_rope=False, q_out=rms)
+        ops.qk_rmsnorm_rope(q=src, gamma_q=gamma, use_rope=False, q_out=rms)
         n_rope = out.float().reshape(T, H, D // 2, 2).square().sum(-1).sqrt()
         n_rms = rms.float().reshape(T, H, D // 2, 2).square().sum(-1).sqrt()
         err = ((n_rope - n_rms).abs() / n_rms.clamp(min=1.0)).max().item()

@@ -137,21 +137,29 @@ def test_empty_rows_zero_pads(dev):
         assert t.numel() == h * 64 * d and not t.any()
 
 
-@pytest.mark.parametrize("k_transposed", [True, False])
+@pytest.mark.parametrize("k_transposed", [1, 0])
 def test_empty_rows_with_rope_sources(dev, k_transposed):
-    """rows = 0 with RoPE on and a non-NULL coords pointer (a zero-row view of
-    a larger coords tensor) or a phase table: no coordinate, phase or row is
-    read, and every output row is a zero pad."""
-    h, d = 4, 128
-    qkv = torch.empty((0, 3 * h * d), device=dev)
-    q, k, v = _views(qkv, h, d)
-    coords = torch.zeros((16, 4), dtype=torch.int32, device=dev)[:0]
-    assert coords.data_ptr() != 0 and coords.is_contiguous()
+    """rows = 0 with RoPE on and a non-NULL coords pointer (a caller's
+    buffer of other rows) or a phase table, through the C ABI: no coordinate,
+    phase or row is read, and every output row is a zero pad. (A zero-row
+    torch view has a NULL data pointer, so the call is made directly.)"""
+    from t2h._lib import call
+
+    h, d, lp = 4, 128, 64
+    freqs, fp, fd = ops._host_freqs(nn.rope_freqs(d))
+    coords = torch.zeros((16, 4), dtype=torch.int32, device=dev)
     phases = torch.ones((1, d // 2, 2), device=dev)
-    for src in (dict(coords=coords), dict(phases=phases)):
-        qh, ko, vh = ops.attn_pack(q, k, v, mp=64, lp=64, freqs=nn.rope_freqs(d), k_transposed=k_transposed, **src)
+    src = torch.zeros((1, 3 * h * d), device=dev)   # input pointers (never read)
+    for ph, ph_rows, co, cc in ((None, 0, coords.data_ptr(), 4), (phases.data_ptr(), 1, None, 0)):
+        qh = torch.full((h, lp, d), 7.0, device=dev)
+        ko = torch.full((h, lp, d), 7.0, device=dev)
+        vh = torch.full((h, lp, d), 7.0, device=dev)
+        call("t2h_attn_pack", src.data_ptr(), src.data_ptr(), src.data_ptr(), 3 * h * d, 0, h, d, 0, None, None,
+             None, None, None, 1, fp, fd, 3, ph, ph_rows, co, cc, 0, qh.data_ptr(), lp, ko.data_ptr(),
+             vh.data_ptr(), lp, k_transposed, ops._stream())
         for t in (qh, ko, vh):
-            assert t.numel() == h * 64 * d and not t.any()
+            assert not t.any()
+    del freqs
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])

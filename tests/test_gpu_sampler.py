@@ -93,9 +93,52 @@ def test_step_rescale_varlen_config4(dev, dtype):
     assert max_err(x0, storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_step_rescale_config5_latent(dev, dtype):
+    """The config-5 token rows (T = 201,436) x 32 latent channels as one
+    varlen segment (6.4M elements: the statistics pass caps a segment at 256
+    blocks, so each block strides over two 16K-element chunks), and the same
+    state split into three segments of unequal sizes; two calls give the
+    same bits (fixed-order sums).
+
+    Bars. The reference sums the std serially in f32; over a 6.4M-element
+    segment that sum is itself off from the exact value: on this case the
+    oracle's x_prev differs by 2.4e-5 from the same step with a float64
+    ratio. The device sums in f64, so against the oracle the f32 bar here is
+    3e-5 / cc (f16: 2e-3 / cc). The defining property is checked tightly in
+    float64 on the device output: with guidance_rescale 1, each segment's
+    x_0 = a*x - cc*x_prev-derived prediction has the positive branch's std
+    (relative 2e-6 for f32 storage)."""
+    coords, offsets = workloads.config5()
+    T = int(offsets[-1])
+    shape = (T, 32)
+    x, pos, neg = _case(3700, shape, dtype)
+    t, tp = 0.81, 0.72
+    cc = float(np.float32(SM + (1 - SM) * t))
+    tol = 3e-5 if dtype == torch.float32 else 2e-3
+    dx, dp, dn = (to_dev(a, dev, dtype) for a in (x, pos, neg))
+    for segs in (np.array([0, T], np.int64), np.array([0, 1000, 150001, T], np.int64)):
+        pred = orc.flow_rescale(x, orc.flow_cfg(pos, neg, 3.0), pos, t, SM, 0.5, segs)
+        outs = [ops.flow_euler_step(dx, dp, t, tp, SM, v_neg=dn, guidance_strength=3.0, guidance_rescale=0.5,
+                                    seg_offsets=segs) for _ in range(2)]
+        xp, x0 = outs[0]
+        assert torch.equal(xp, outs[1][0]) and torch.equal(x0, outs[1][1])
+        assert max_err(xp, storage_round(orc.flow_step(x, pred, t, tp), dtype)) <= tol / cc
+        assert max_err(x0, storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
+    if dtype == torch.float32:
+        segs = np.array([0, 1000, 150001, T], np.int64)
+        _, x0 = ops.flow_euler_step(dx, dp, t, tp, SM, v_neg=dn, guidance_strength=3.0, guidance_rescale=1.0,
+                                    seg_offsets=segs)
+        x0d = host(x0).astype(np.float64)
+        x0p = np.float32(1 - SM) * x - np.float32(cc) * pos
+        for lo, hi in zip(segs[:-1], segs[1:]):
+            assert abs(x0d[lo:hi].std() / x0p[lo:hi].astype(np.float64).std() - 1) < 2e-6
+
+
 def test_step_odd_rows_and_unaligned_state(dev):
-    """Rows of 12,289 elements (three 4,096-element statistics blocks and a
-    1-element tail block per row, rows starting at odd element offsets), and
+    """Rows of 12,289 elements (one statistics block per row; three
+    4,096-element elementwise blocks and a 1-element tail block per row; rows
+    starting at odd element offsets, so the scalar path runs), and
     the same state viewed one element into its buffer (no 16-byte
     alignment): the oracle's bits without rescale and its tolerance with it."""
     shape = (3, 12289)

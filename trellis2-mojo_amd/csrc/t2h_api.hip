@@ -702,19 +702,25 @@ int32_t t2h_modulation_add(const float* mod, const float* modulation, float* m, 
     return hip_status(launch_modulation_add(mod, modulation, m, n, width, static_cast<hipStream_t>(stream)), fn);
 }
 
-// Flow-matching Euler step: workspace layout = f64 partials [blocks][4], then
-// f32 ratios [nseg] (16-byte aligned).
-static int64_t euler_ws_bytes(int64_t blocks, int64_t nseg) {
-    return blocks * 32 + ((nseg * 4 + 255) / 256) * 256;
+// Flow-matching Euler step. The rescale's workspace holds the statistics
+// pass's f64 partial quads [nstats][4]: at most kStatsMaxPerSeg per segment.
+static int64_t stats_blocks(int64_t m) {
+    const int64_t c = (m + kStatsChunk - 1) / kStatsChunk;
+    return c < kStatsMaxPerSeg ? c : kStatsMaxPerSeg;
 }
 
 int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size, int32_t n_seg_offsets) {
     if (rows < 0 || row_size < 0 || n_seg_offsets < 0) return -1;
-    const int64_t nseg = n_seg_offsets > 0 ? n_seg_offsets - 1 : rows;
-    const int64_t per_row = (row_size + kEulerChunk - 1) / kEulerChunk;
-    const int64_t blocks = n_seg_offsets > 0 ? (rows * row_size + kEulerChunk - 1) / kEulerChunk + nseg
-                                              : rows * per_row;
-    return euler_ws_bytes(blocks, nseg);
+    int64_t blocks;
+    if (n_seg_offsets > 0) {   // segment sizes unknown here: the largest total over any split
+        const int64_t nseg = n_seg_offsets - 1;
+        const int64_t a = nseg * (int64_t)kStatsMaxPerSeg;
+        const int64_t b = (rows * row_size + kStatsChunk - 1) / kStatsChunk + nseg;
+        blocks = a < b ? a : b;
+    } else {
+        blocks = rows * stats_blocks(row_size);
+    }
+    return blocks * 32;
 }
 
 int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev, void* pred_x0,
@@ -752,8 +758,14 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_ne
     a.dt = (float)(t - t_prev);
     a.gr = (float)guidance_rescale;
     a.one_m_gr = 1.0f - a.gr;
-    int64_t blocks = 0, cover_lo = 0, cover_hi = n;
+    // vector path: 16-byte aligned tensors and block bounds on whole vectors
+    const int64_t ve = dtype == T2H_F32 ? 4 : 8;
+    const bool al = T2H_EULER_VEC && aligned(a.x, 16) && aligned(a.v_pos, 16) && (a.mode == 0 || aligned(a.v_neg, 16)) &&
+                    aligned(x_prev, 16) && aligned(pred_x0, 16);
+    int64_t cover_lo = 0, cover_hi = n;
     if (a.mode == 2) {
+        bool bounds_al = true;
+        int64_t blocks = 0, stats = 0;
         if (n_seg_offsets > 0) {
             if (seg_offsets_host == nullptr) return fail(T2H_EINVAL, "%s: NULL seg_offsets", fn);
             const int nseg = n_seg_offsets - 1;
@@ -763,33 +775,43 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_ne
                 if (o < 0 || o > rows || (s > 0 && o < seg_offsets_host[s - 1]))
                     return fail(T2H_EINVAL, "%s: seg_offsets must be ordered within [0, rows]", fn);
                 a.bounds[s] = o * row_size;
+                bounds_al = bounds_al && a.bounds[s] % ve == 0;
             }
             a.uniform = 0;
             a.nseg = nseg;
             for (int s = 0; s < nseg; ++s) {
+                const int64_t m = a.bounds[s + 1] - a.bounds[s];
                 a.blk_base[s] = blocks;
-                blocks += (a.bounds[s + 1] - a.bounds[s] + kEulerChunk - 1) / kEulerChunk;
+                a.pbase[s] = stats;
+                blocks += (m + kEulerChunk - 1) / kEulerChunk;
+                stats += stats_blocks(m);
             }
             a.blk_base[nseg] = blocks;
+            a.pbase[nseg] = stats;
             cover_lo = a.bounds[0];
             cover_hi = a.bounds[nseg];
         } else {
             a.uniform = 1;
             if (rows > INT32_MAX) return fail(T2H_EUNSUPPORTED, "%s: too many rows", fn);
             a.nseg = (int32_t)rows;
+            a.pper = (int32_t)stats_blocks(row_size);
             blocks = rows * ((row_size + kEulerChunk - 1) / kEulerChunk);
+            stats = rows * a.pper;
+            bounds_al = row_size % ve == 0;
         }
-        const int64_t need = euler_ws_bytes(blocks, a.nseg);
+        const int64_t need = stats * 32;
         if (workspace == nullptr || workspace_bytes < need)
             return fail(T2H_EINVAL, "%s: rescale needs a %lld-byte workspace", fn, (long long)need);
         if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(T2H_EINVAL, "%s: workspace alignment", fn);
         a.partial = static_cast<double*>(workspace);
-        a.ratio = reinterpret_cast<float*>(static_cast<char*>(workspace) + blocks * 32);
         a.nblocks = blocks;
+        a.nstats = stats;
+        a.vec = al && bounds_al ? 1 : 0;
     } else {
-        a.nblocks = (n + kEulerChunkPlain - 1) / kEulerChunkPlain;
+        a.nblocks = (n + kEulerChunk - 1) / kEulerChunk;
+        a.vec = al && n % ve == 0 ? 1 : 0;
     }
-    return hip_status(launch_euler(a, blocks, cover_lo, cover_hi, static_cast<hipStream_t>(stream)), fn);
+    return hip_status(launch_euler(a, cover_lo, cover_hi, static_cast<hipStream_t>(stream)), fn);
 }
 
 // Resident-block glue over one const buffer: the pair at `off` is

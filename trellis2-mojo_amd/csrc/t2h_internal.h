@@ -129,9 +129,28 @@ struct GemmArgs {
 };
 
 // Flow-matching Euler step (t2h_flow_euler_step).
-constexpr int kEulerChunk = 4096;        // elements per block of the rescale's two passes
-constexpr int kEulerChunkPlain = 2048;   // elements per block without the rescale
-constexpr int kEulerMaxSeg = 64;    // varlen segments carried in the kernel arguments
+constexpr int kEulerBlock = 256;          // threads per block of the elementwise pass
+#ifndef T2H_EULER_CHUNK
+#define T2H_EULER_CHUNK 2048
+#endif
+#ifndef T2H_EULER_VEC
+#define T2H_EULER_VEC 1   // 0: the scalar path for every call (tuning comparisons)
+#endif
+#ifndef T2H_STATS_PER
+#define T2H_STATS_PER 16
+#endif
+constexpr int kEulerChunk = T2H_EULER_CHUNK;   // elements per block of the elementwise pass
+#ifndef T2H_STATS_BLOCK
+#define T2H_STATS_BLOCK 1024
+#endif
+#ifndef T2H_STATS_MAXSEG
+#define T2H_STATS_MAXSEG 256
+#endif
+constexpr int kStatsBlock = T2H_STATS_BLOCK;   // threads per block of the rescale's statistics pass
+constexpr int kStatsPer = T2H_STATS_PER;  // elements per thread per statistics load group
+constexpr int kStatsChunk = kStatsBlock * kStatsPer;   // 16384 elements
+constexpr int kStatsMaxPerSeg = T2H_STATS_MAXSEG;   // statistics blocks (f64 partials) per segment, at most
+constexpr int kEulerMaxSeg = 64;          // varlen segments carried in the kernel arguments
 struct EulerArgs {
     const void* x;
     const void* v_pos;
@@ -145,13 +164,17 @@ struct EulerArgs {
     float gp, gn;            // f32(g), f32(1 - g)
     float a, cc, dt;         // f32(1 - sigma_min), f32(sigma_min + (1 - sigma_min) t), f32(t - t_prev)
     float gr, one_m_gr;      // f32(guidance_rescale), 1 - that (in f32)
+    int32_t vec;             // 1: every tensor 16-byte aligned and every block bound a multiple
+                             //    of the 16-byte element count -> vector loads/stores
     int32_t uniform;         // 1: segment = row (dense), 0: bounds[] (varlen)
     int32_t nseg;
     int64_t bounds[kEulerMaxSeg + 1];    // element bounds of the varlen segments
-    int64_t blk_base[kEulerMaxSeg + 1];  // first block of each segment
-    int64_t nblocks;         // blocks of the statistics / elementwise passes
-    double* partial;         // [blocks][4] workspace
-    float* ratio;            // [nseg] workspace
+    int64_t blk_base[kEulerMaxSeg + 1];  // first elementwise block of each varlen segment
+    int64_t pbase[kEulerMaxSeg + 1];     // first statistics block (partial) of each varlen segment
+    int32_t pper;            // statistics blocks per row (uniform)
+    int64_t nblocks;         // blocks of the elementwise pass
+    int64_t nstats;          // blocks of the statistics pass (= f64 partials)
+    double* partial;         // [nstats][4] workspace: sum x0_pos, sum x0_pos^2, sum x0_cfg, sum x0_cfg^2
 };
 
 struct PhaseArgs {
@@ -206,7 +229,7 @@ int32_t gemm_head_dim();       // head_dim of the fused qkv GEMM + pack
 hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_gemm_residual(GemmArgs a, hipStream_t s);
 // t2h_sampler.hip
-hipError_t launch_euler(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
+hipError_t launch_euler(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
 // t2h_eltwise.hip
 hipError_t launch_activation(const EltArgs& a, hipStream_t s);
 hipError_t launch_gate_residual(const EltArgs& a, hipStream_t s);

@@ -1,7 +1,7 @@
 // One flow-matching Euler step of the sampler over a flat state x_t:
 // classifier-free-guidance combine, optional CFG rescale, the Euler update and
-// the x_0 prediction, in one elementwise pass (plus, for the rescale, a
-// statistics pass and a per-segment ratio).
+// the x_0 prediction, in one elementwise pass (plus, for the rescale, one
+// statistics pass in front of it).
 //
 //   pred   = v_pos (no guidance) or fl(v_pos * f32(g)) + fl(v_neg * f32(1-g))
 //   rescale (guidance_rescale > 0):
@@ -12,9 +12,25 @@
 //   pred_x0 = fl(x*a) - fl(pred*cc)
 // with a = f32(1 - sigma_min), cc = f32(sigma_min + (1 - sigma_min) t).
 // Segments are rows of row_size elements (dense state, unbiased std) or the
-// caller's token segments (varlen state, biased std). The statistics are
-// summed in f64 per block of kChunk elements, then per segment in a fixed
-// order, so the result is deterministic.
+// caller's token segments (varlen state, biased std).
+//
+// The rescale takes two launches:
+// - euler_stats_kernel: at most kStatsMaxPerSeg blocks of 1024 threads per
+//   segment (one per 16K elements) take equal shares of it, load them with
+//   16-byte loads, sum
+//   x0_pos, x0_pos^2, x0_cfg, x0_cfg^2 in f64 per thread, reduce through DPP
+//   row sums and one LDS combine, and write one f64 partial quad per block.
+//   Its loads are ordinary (cached), so the elementwise pass that re-reads
+//   the same 3 tensors right after finds them in the infinity cache when
+//   they fit.
+// - euler_apply_kernel: each block (2048 elements) first sums its segment's
+//   partials (at most 256 quads, one per thread, fixed order) into the
+//   segment's ratio,
+//   with its own element loads already in flight, then runs the elementwise
+//   step. Every block of a segment sums the same partials in the same order,
+//   so all of them compute the same ratio bits, and the result is
+//   deterministic.
+// Without the rescale there is only the elementwise pass.
 //
 // Reference: samplers/flow_euler.mojo:56-57 (_scaled), 68-70
 // (_v_to_xstart), 75-149 (_rescale_pred), 151-181 (_inference),
@@ -22,81 +38,136 @@
 #include "t2h_device.h"
 #include "t2h_internal.h"
 
+#ifndef T2H_EULER_NTL
+#define T2H_EULER_NTL 0   // elementwise pass: non-temporal loads (measured slower: 21.9 vs 19.8 us)
+#endif
+#ifndef T2H_EULER_NTS
+#define T2H_EULER_NTS 1   // elementwise pass: non-temporal stores
+#endif
+
 namespace t2h {
 namespace {
-
-constexpr int kEulerBlock = 256;
-
-// Segment bounds of block b: blocks tile every segment in kEulerChunk pieces.
-struct SegMap {
-    __device__ __forceinline__ static void locate(const EulerArgs& a, int64_t b, int& s, int64_t& lo, int64_t& hi) {
-        if (a.uniform) {
-            const int64_t nb = (a.row_size + kEulerChunk - 1) / kEulerChunk;
-            s = (int)(b / nb);
-            const int64_t j = b % nb;
-            lo = s * a.row_size + j * kEulerChunk;
-            hi = min(lo + kEulerChunk, (s + 1) * a.row_size);
-        } else {
-            s = 0;
-            while (s + 1 < a.nseg && a.blk_base[s + 1] <= b) ++s;
-            const int64_t j = b - a.blk_base[s];
-            lo = a.bounds[s] + j * kEulerChunk;
-            hi = min(lo + kEulerChunk, a.bounds[s + 1]);
-        }
-    }
-};
-
-template <typename T>
-__device__ __forceinline__ float cfg_pred(const EulerArgs& a, int64_t e, float& pos) {
-    pos = ld1(static_cast<const T*>(a.v_pos) + e);
-    if (a.mode == 0) return pos;
-    const float neg = ld1(static_cast<const T*>(a.v_neg) + e);
-    return add_rn(mul_rn(pos, a.gp), mul_rn(neg, a.gn));
-}
 
 __device__ __forceinline__ float v_to_x0(float x, float v, float a, float cc) {
     return sub_rn(mul_rn(x, a), mul_rn(v, cc));
 }
 
-// f64 block sum of 4 values through LDS, result in thread 0.
+// f64 DPP move of both 32-bit halves.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Wave64 sum of an f64 (all lanes active); wave-uniform result, fixed order.
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v += dpp_d<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_d<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_d<0x141>(v);   // row_half_mirror
+    v += dpp_d<0x140>(v);   // row_mirror
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
+// Block sum of 4 f64 values (all threads of the block take part); every
+// thread gets the totals, summed over the waves in wave order.
+template <int NW>
 __device__ __forceinline__ void block_sum4(double (&v)[4], double (*sh)[4]) {
-    const int t = threadIdx.x;
+    const int w = threadIdx.x >> 6;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) sh[t][k] = v[k];
-    __syncthreads();
-    for (int w = kEulerBlock / 2; w > 0; w >>= 1) {
-        if (t < w) {
+    for (int k = 0; k < 4; ++k) v[k] = wave_sum_d(v[k]);
+    if ((threadIdx.x & 63) == 0) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) sh[t][k] += sh[t + w][k];
-        }
-        __syncthreads();
+        for (int k = 0; k < 4; ++k) sh[w][k] = v[k];
     }
+    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = sh[0][k];
+    for (int k = 0; k < 4; ++k) {
+        double s = sh[0][k];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) s += sh[i][k];
+        v[k] = s;
+    }
+}
+
+// x0_pos / x0_cfg contributions of one element to the four sums.
+__device__ __forceinline__ void stats_add(const EulerArgs& a, float xv, float pos, float neg, double (&acc)[4]) {
+    const float pred = add_rn(mul_rn(pos, a.gp), mul_rn(neg, a.gn));
+    const double x0p = v_to_x0(xv, pos, a.a, a.cc);
+    const double x0c = v_to_x0(xv, pred, a.a, a.cc);
+    acc[0] += x0p;
+    acc[1] += x0p * x0p;   // exact: a product of two f32 fits an f64
+    acc[2] += x0c;
+    acc[3] += x0c * x0c;
 }
 
 template <typename T>
-__global__ __launch_bounds__(kEulerBlock) void euler_stats_kernel(EulerArgs a) {
-    __shared__ double sh[kEulerBlock][4];
+__global__ __launch_bounds__(kStatsBlock) void euler_stats_kernel(EulerArgs a) {
+    constexpr int NW = kStatsBlock / 64;
+    __shared__ double sh[NW][4];
     const int64_t b = block_linear();
-    if (b >= a.nblocks) return;
-    int s;
-    int64_t lo, hi;
-    SegMap::locate(a, b, s, lo, hi);
-    const T* __restrict__ x = static_cast<const T*>(a.x);
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int64_t e = lo + threadIdx.x; e < hi; e += kEulerBlock) {
-        float pos;
-        const float pred = cfg_pred<T>(a, e, pos);
-        const float xv = ld1(x + e);
-        const double x0p = v_to_x0(xv, pos, a.a, a.cc);
-        const double x0c = v_to_x0(xv, pred, a.a, a.cc);
-        acc[0] += x0p;
-        acc[1] += x0p * x0p;
-        acc[2] += x0c;
-        acc[3] += x0c * x0c;
+    if (b >= a.nstats) return;   // block-uniform
+    int64_t j, per, lo, hi;
+    if (a.uniform) {
+        per = a.pper;
+        const int64_t s = b / per;
+        j = b - s * per;
+        lo = s * a.row_size;
+        hi = lo + a.row_size;
+    } else {
+        int s = 0;
+        while (s + 1 < a.nseg && a.pbase[s + 1] <= b) ++s;
+        j = b - a.pbase[s];
+        per = a.pbase[s + 1] - a.pbase[s];
+        lo = a.bounds[s];
+        hi = a.bounds[s + 1];
     }
-    block_sum4(acc, sh);
+    // the segment's `per` blocks take equal shares of whole vectors
+    constexpr int V = kPack<T>;
+    const int64_t share = ((hi - lo + V - 1) / V + per - 1) / per * V;
+    const int64_t c0 = lo + j * share;
+    const int64_t c1 = c0 + share < hi ? c0 + share : hi;
+    const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* __restrict__ vp = static_cast<const T*>(a.v_pos);
+    const T* __restrict__ vn = static_cast<const T*>(a.v_neg);
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    if (a.vec) {
+        // c0 and c1 are multiples of V: every vector lies inside [c0, c1);
+        // a group's loads past c1 are clamped to the last vector
+        // (unconditional loads stay in flight together) and not summed
+        constexpr int NV = kStatsPer / V;
+        for (int64_t g0 = c0; g0 < c1; g0 += (int64_t)kStatsBlock * V * NV) {
+            float xv[NV][V], pv[NV][V], nv[NV][V];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int64_t e = g0 + ((int64_t)i * kStatsBlock + threadIdx.x) * V;
+                const int64_t el = e < c1 ? e : c1 - V;
+                load_elems<T, V>(x + el, xv[i]);
+                load_elems<T, V>(vp + el, pv[i]);
+                load_elems<T, V>(vn + el, nv[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int64_t e = g0 + ((int64_t)i * kStatsBlock + threadIdx.x) * V;
+                if (e < c1) {
+#pragma unroll
+                    for (int k = 0; k < V; ++k) stats_add(a, xv[i][k], pv[i][k], nv[i][k], acc);
+                }
+            }
+        }
+    } else {
+        for (int64_t e = c0 + threadIdx.x; e < c1; e += kStatsBlock)
+            stats_add(a, ld1(x + e), ld1(vp + e), ld1(vn + e), acc);
+    }
+    block_sum4<NW>(acc, sh);
     if (threadIdx.x == 0) {
         double* p = a.partial + b * 4;
 #pragma unroll
@@ -104,72 +175,118 @@ __global__ __launch_bounds__(kEulerBlock) void euler_stats_kernel(EulerArgs a) {
     }
 }
 
-// One block per segment: fixed-order sum of the segment's block partials.
-__global__ __launch_bounds__(kEulerBlock) void euler_ratio_kernel(EulerArgs a) {
-    __shared__ double sh[kEulerBlock][4];
-    const int64_t sl = block_linear();
-    if (sl >= a.nseg) return;
-    const int s = (int)sl;
-    int64_t b0, b1, m;
+// The rescale ratio of segment s from its partials (called by every thread
+// of a kEulerBlock-thread block; the same bits in every block).
+__device__ __forceinline__ float segment_ratio(const EulerArgs& a, int s, double (*sh)[4]) {
+    int64_t p0, np, m;
     if (a.uniform) {
-        const int64_t nb = (a.row_size + kEulerChunk - 1) / kEulerChunk;
-        b0 = s * nb;
-        b1 = b0 + nb;
+        p0 = (int64_t)s * a.pper;
+        np = a.pper;
         m = a.row_size;
     } else {
-        b0 = a.blk_base[s];
-        b1 = a.blk_base[s + 1];
+        p0 = a.pbase[s];
+        np = a.pbase[s + 1] - p0;
         m = a.bounds[s + 1] - a.bounds[s];
     }
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int64_t b = b0 + threadIdx.x; b < b1; b += kEulerBlock) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) acc[k] += a.partial[b * 4 + k];
+    for (int64_t i = threadIdx.x; i < np; i += kEulerBlock) {   // fixed order per thread
+        const double2* q = reinterpret_cast<const double2*>(a.partial + (p0 + i) * 4);
+        const double2 u = q[0], w = q[1];
+        acc[0] += u.x; acc[1] += u.y; acc[2] += w.x; acc[3] += w.y;
     }
-    block_sum4(acc, sh);
-    if (threadIdx.x == 0) {
-        const double md = (double)m;
-        double vp, vc;
-        if (a.uniform) {   // unbiased, one segment per row
-            vp = (acc[1] - acc[0] * (acc[0] / md)) / (md - 1.0);
-            vc = (acc[3] - acc[2] * (acc[2] / md)) / (md - 1.0);
-        } else {           // biased: mean(x^2) - mean(x)^2
-            vp = acc[1] / md - (acc[0] / md) * (acc[0] / md);
-            vc = acc[3] / md - (acc[2] / md) * (acc[2] / md);
-        }
-        a.ratio[s] = m > 0 ? (float)(sqrt(vp > 0.0 ? vp : 0.0) / sqrt(vc > 0.0 ? vc : 0.0)) : 0.0f;
-        if (a.uniform && m == 1) a.ratio[s] = __builtin_nanf("");   // 0/0 as the reference's m - 1 = 0
+    block_sum4<kEulerBlock / 64>(acc, sh);
+    const double md = (double)m;
+    double vp, vc;
+    if (a.uniform) {   // unbiased, one segment per row
+        vp = (acc[1] - acc[0] * (acc[0] / md)) / (md - 1.0);
+        vc = (acc[3] - acc[2] * (acc[2] / md)) / (md - 1.0);
+    } else {           // biased: mean(x^2) - mean(x)^2
+        vp = acc[1] / md - (acc[0] / md) * (acc[0] / md);
+        vc = acc[3] / md - (acc[2] / md) * (acc[2] / md);
     }
+    if (a.uniform && m == 1) return __builtin_nanf("");   // 0/0 as the reference's m - 1 = 0
+    return (float)(sqrt(vp > 0.0 ? vp : 0.0) / sqrt(vc > 0.0 ? vc : 0.0));
 }
 
-template <typename T>
+template <int MODE>
+__device__ __forceinline__ void apply_elem(const EulerArgs& a, float ratio, float xv, float pos, float neg,
+                                           float& xprev, float& x0) {
+    float pred = MODE == 0 ? pos : add_rn(mul_rn(pos, a.gp), mul_rn(neg, a.gn));
+    if (MODE == 2) {
+        const float x0c = v_to_x0(xv, pred, a.a, a.cc);
+        const float x0r = mul_rn(x0c, ratio);
+        const float x0b = add_rn(mul_rn(a.gr, x0r), mul_rn(a.one_m_gr, x0c));
+        pred = __fdiv_rn(sub_rn(mul_rn(a.a, xv), x0b), a.cc);
+    }
+    xprev = sub_rn(xv, mul_rn(pred, a.dt));
+    x0 = v_to_x0(xv, pred, a.a, a.cc);
+}
+
+template <typename T, int MODE>
 __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
+    __shared__ double sh[kEulerBlock / 64][4];
     const T* __restrict__ x = static_cast<const T*>(a.x);
+    const T* __restrict__ vp = static_cast<const T*>(a.v_pos);
+    const T* __restrict__ vn = static_cast<const T*>(a.v_neg);
     T* __restrict__ xp = static_cast<T*>(a.x_prev);
     T* __restrict__ x0o = static_cast<T*>(a.pred_x0);
     const int64_t b = block_linear();
-    if (b >= a.nblocks) return;
+    if (b >= a.nblocks) return;   // block-uniform
     int s = 0;
     int64_t lo, hi;
-    if (a.mode == 2) {
-        SegMap::locate(a, b, s, lo, hi);
-    } else {
-        lo = b * kEulerChunkPlain;
-        hi = min(lo + kEulerChunkPlain, a.n);
-    }
-    const float ratio = a.mode == 2 ? a.ratio[s] : 0.0f;
-    for (int64_t e = lo + threadIdx.x; e < hi; e += kEulerBlock) {
-        const float xv = ld1(x + e);
-        float pos;
-        float pred = cfg_pred<T>(a, e, pos);
-        if (a.mode == 2) {
-            const float x0c = v_to_x0(xv, pred, a.a, a.cc);
-            const float x0r = mul_rn(x0c, ratio);
-            const float x0 = add_rn(mul_rn(a.gr, x0r), mul_rn(a.one_m_gr, x0c));
-            pred = __fdiv_rn(sub_rn(mul_rn(a.a, xv), x0), a.cc);
+    if (MODE == 2) {
+        int64_t j;
+        if (a.uniform) {
+            const int64_t nb = (a.row_size + kEulerChunk - 1) / kEulerChunk;
+            s = (int)(b / nb);
+            j = b - (int64_t)s * nb;
+            lo = (int64_t)s * a.row_size + j * kEulerChunk;
+            hi = (int64_t)(s + 1) * a.row_size;
+        } else {
+            while (s + 1 < a.nseg && a.blk_base[s + 1] <= b) ++s;
+            j = b - a.blk_base[s];
+            lo = a.bounds[s] + j * kEulerChunk;
+            hi = a.bounds[s + 1];
         }
-        st1(xp + e, sub_rn(xv, mul_rn(pred, a.dt)));
-        if (x0o != nullptr) st1(x0o + e, v_to_x0(xv, pred, a.a, a.cc));
+    } else {
+        lo = b * kEulerChunk;
+        hi = a.n;
+    }
+    hi = lo + kEulerChunk < hi ? lo + kEulerChunk : hi;
+
+    if (a.vec) {
+        constexpr int V = kPack<T>;
+        constexpr int NV = kEulerChunk / kEulerBlock / V;
+        float xv[NV][V], pv[NV][V], nv[NV][V];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int64_t e = lo + ((int64_t)i * kEulerBlock + threadIdx.x) * V;
+            const int64_t el = e < hi ? e : hi - V;
+            load_elems<T, V, T2H_EULER_NTL>(x + el, xv[i]);
+            load_elems<T, V, T2H_EULER_NTL>(vp + el, pv[i]);
+            if (MODE != 0) load_elems<T, V, T2H_EULER_NTL>(vn + el, nv[i]);
+        }
+        const float ratio = MODE == 2 ? segment_ratio(a, s, sh) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int64_t e = lo + ((int64_t)i * kEulerBlock + threadIdx.x) * V;
+            float o[V], z[V];
+#pragma unroll
+            for (int k = 0; k < V; ++k)
+                apply_elem<MODE>(a, ratio, xv[i][k], pv[i][k], MODE != 0 ? nv[i][k] : 0.0f, o[k], z[k]);
+            if (e < hi) {
+                store_elems<T, V, T2H_EULER_NTS>(xp + e, o);
+                if (x0o != nullptr) store_elems<T, V, T2H_EULER_NTS>(x0o + e, z);
+            }
+        }
+    } else {
+        const float ratio = MODE == 2 ? segment_ratio(a, s, sh) : 0.0f;
+        for (int64_t e = lo + threadIdx.x; e < hi; e += kEulerBlock) {
+            float o, z;
+            apply_elem<MODE>(a, ratio, ld1(x + e), ld1(vp + e), MODE != 0 ? ld1(vn + e) : 0.0f, o, z);
+            st1(xp + e, o);
+            if (x0o != nullptr) st1(x0o + e, z);
+        }
     }
 }
 
@@ -189,12 +306,11 @@ __global__ __launch_bounds__(kEulerBlock) void euler_uncovered_kernel(EulerArgs 
 }
 
 template <typename T>
-hipError_t launch_typed(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t st) {
+hipError_t launch_typed(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, hipStream_t st) {
     if (a.mode == 2) {
-        if (blocks > 0) {
-            hipLaunchKernelGGL(euler_stats_kernel<T>, grid_1d(blocks), dim3(kEulerBlock), 0, st, a);
-            hipLaunchKernelGGL(euler_ratio_kernel, grid_1d(a.nseg), dim3(kEulerBlock), 0, st, a);
-            hipLaunchKernelGGL(euler_apply_kernel<T>, grid_1d(blocks), dim3(kEulerBlock), 0, st, a);
+        if (a.nblocks > 0) {
+            hipLaunchKernelGGL(euler_stats_kernel<T>, grid_1d(a.nstats), dim3(kStatsBlock), 0, st, a);
+            hipLaunchKernelGGL((euler_apply_kernel<T, 2>), grid_1d(a.nblocks), dim3(kEulerBlock), 0, st, a);
         }
         if (cover_lo > 0) {
             const int64_t g = (cover_lo + kEulerBlock - 1) / kEulerBlock;
@@ -206,19 +322,21 @@ hipError_t launch_typed(const EulerArgs& a, int64_t blocks, int64_t cover_lo, in
             hipLaunchKernelGGL(euler_uncovered_kernel<T>, dim3((unsigned)(g < 4096 ? g : 4096)), dim3(kEulerBlock),
                                0, st, a, cover_hi, a.n);
         }
+    } else if (a.mode == 1) {
+        hipLaunchKernelGGL((euler_apply_kernel<T, 1>), grid_1d(a.nblocks), dim3(kEulerBlock), 0, st, a);
     } else {
-        hipLaunchKernelGGL(euler_apply_kernel<T>, grid_1d(a.nblocks), dim3(kEulerBlock), 0, st, a);
+        hipLaunchKernelGGL((euler_apply_kernel<T, 0>), grid_1d(a.nblocks), dim3(kEulerBlock), 0, st, a);
     }
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_euler(const EulerArgs& a, int64_t blocks, int64_t cover_lo, int64_t cover_hi, hipStream_t s) {
+hipError_t launch_euler(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, hipStream_t s) {
     switch (a.dtype) {
-        case T2H_F32: return launch_typed<float>(a, blocks, cover_lo, cover_hi, s);
-        case T2H_F16: return launch_typed<_Float16>(a, blocks, cover_lo, cover_hi, s);
-        default: return launch_typed<__bf16>(a, blocks, cover_lo, cover_hi, s);
+        case T2H_F32: return launch_typed<float>(a, cover_lo, cover_hi, s);
+        case T2H_F16: return launch_typed<_Float16>(a, cover_lo, cover_hi, s);
+        default: return launch_typed<__bf16>(a, cover_lo, cover_hi, s);
     }
 }
 
