@@ -352,6 +352,28 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos,
                             int32_t n_seg_offsets, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: t2h_flow_euler_step for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments without the
+ * workspace: the rescale's statistics go to a scratch array built into the
+ * library, 512 KB per GPU (16,384 statistics blocks: every varlen split of
+ * up to 64 segments, or up to 16,384 dense rows of <= 16,384 elements each;
+ * larger dense states return T2H_EUNSUPPORTED). It allocates nothing, and
+ * its results equal t2h_flow_euler_step's bit for bit. Every call on a GPU
+ * shares that GPU's scratch, so calls that overlap on one GPU (other
+ * streams, other threads) race; stream-ordered calls do not. Call
+ * t2h_device_init first to do the one-time per-device scratch lookup
+ * outside any capture. */
+int32_t t2h_flow_euler_step_noalloc(const void* x_t, const void* v_pos,
+                                    const void* v_neg, void* x_prev,
+                                    void* pred_x0, int64_t rows,
+                                    int64_t row_size, int32_t dtype, double t,
+                                    double t_prev, double sigma_min,
+                                    double guidance_strength,
+                                    double guidance_rescale,
+                                    const int64_t* seg_offsets_host,
+                                    int32_t n_seg_offsets, void* stream);
+
 /* ---- resident-block glue over one const buffer ---------------------------
  * The device-resident DiT cross block keeps its per-block glue constants in
  * one f32 buffer `consts` of 12*C floats (gpu/block.mojo:255-289): pairs of

@@ -146,6 +146,9 @@ int32_t t2h_device_init(int32_t device) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(T2H_EDEVICE, "t2h_device_init: device %d is %s, libt2h is built for gfx950", device, prop.gcnArchName);
     (void)device_cu_count();
+    double* scratch = nullptr;   // t2h_flow_euler_step_noalloc's scratch on this device
+    e = euler_scratch(&scratch);
+    if (e != hipSuccess) return hip_status(e, "t2h_device_init");
     return ok();
 }
 
@@ -723,12 +726,13 @@ int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size, int32_t n_seg_o
     return blocks * 32;
 }
 
-int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev, void* pred_x0,
-                            int64_t rows, int64_t row_size, int32_t dtype, double t, double t_prev,
-                            double sigma_min, double guidance_strength, double guidance_rescale,
-                            const int64_t* seg_offsets_host, int32_t n_seg_offsets, void* workspace,
-                            int64_t workspace_bytes, void* stream) {
-    const char* fn = "t2h_flow_euler_step";
+// builtin: the statistics go to the library's per-device scratch instead of
+// the caller's workspace (t2h_flow_euler_step_noalloc).
+static int32_t euler_step(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev, void* pred_x0,
+                          int64_t rows, int64_t row_size, int32_t dtype, double t, double t_prev, double sigma_min,
+                          double guidance_strength, double guidance_rescale, const int64_t* seg_offsets_host,
+                          int32_t n_seg_offsets, void* workspace, int64_t workspace_bytes, bool builtin,
+                          void* stream, const char* fn) {
     if (!dtype_ok(dtype)) return fail(T2H_EINVAL, "%s: bad dtype %d", fn, dtype);
     if (rows < 0 || row_size <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
     if (n_seg_offsets < 0 || n_seg_offsets == 1) return fail(T2H_EINVAL, "%s: seg_offsets needs >= 2 entries", fn);
@@ -800,6 +804,16 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_ne
             bounds_al = row_size % ve == 0;
         }
         const int64_t need = stats * 32;
+        if (builtin) {
+            if (stats > kEulerScratchPartials)
+                return fail(T2H_EUNSUPPORTED, "%s: the rescale needs %lld statistics blocks; the built-in scratch "
+                            "holds %d (use t2h_flow_euler_step with a workspace)", fn, (long long)stats,
+                            kEulerScratchPartials);
+            double* sp = nullptr;
+            if (hipError_t e = euler_scratch(&sp); e != hipSuccess) return hip_status(e, fn);
+            workspace = sp;
+            workspace_bytes = (int64_t)kEulerScratchPartials * 32;
+        }
         if (workspace == nullptr || workspace_bytes < need)
             return fail(T2H_EINVAL, "%s: rescale needs a %lld-byte workspace", fn, (long long)need);
         if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(T2H_EINVAL, "%s: workspace alignment", fn);
@@ -812,6 +826,26 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_ne
         a.vec = al && n % ve == 0 ? 1 : 0;
     }
     return hip_status(launch_euler(a, cover_lo, cover_hi, static_cast<hipStream_t>(stream)), fn);
+}
+
+int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev, void* pred_x0,
+                            int64_t rows, int64_t row_size, int32_t dtype, double t, double t_prev,
+                            double sigma_min, double guidance_strength, double guidance_rescale,
+                            const int64_t* seg_offsets_host, int32_t n_seg_offsets, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+    return euler_step(x_t, v_pos, v_neg, x_prev, pred_x0, rows, row_size, dtype, t, t_prev, sigma_min,
+                      guidance_strength, guidance_rescale, seg_offsets_host, n_seg_offsets, workspace,
+                      workspace_bytes, false, stream, "t2h_flow_euler_step");
+}
+
+int32_t t2h_flow_euler_step_noalloc(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev,
+                                    void* pred_x0, int64_t rows, int64_t row_size, int32_t dtype, double t,
+                                    double t_prev, double sigma_min, double guidance_strength,
+                                    double guidance_rescale, const int64_t* seg_offsets_host, int32_t n_seg_offsets,
+                                    void* stream) {
+    return euler_step(x_t, v_pos, v_neg, x_prev, pred_x0, rows, row_size, dtype, t, t_prev, sigma_min,
+                      guidance_strength, guidance_rescale, seg_offsets_host, n_seg_offsets, nullptr, 0, true,
+                      stream, "t2h_flow_euler_step_noalloc");
 }
 
 // Resident-block glue over one const buffer: the pair at `off` is

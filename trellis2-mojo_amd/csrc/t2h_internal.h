@@ -151,6 +151,9 @@ constexpr int kStatsPer = T2H_STATS_PER;  // elements per thread per statistics 
 constexpr int kStatsChunk = kStatsBlock * kStatsPer;   // 16384 elements
 constexpr int kStatsMaxPerSeg = T2H_STATS_MAXSEG;   // statistics blocks (f64 partials) per segment, at most
 constexpr int kEulerMaxSeg = 64;          // varlen segments carried in the kernel arguments
+// statistics blocks the built-in scratch of t2h_flow_euler_step_noalloc holds
+// (64 segments at the per-segment cap; 16,384 f64 quads = 512 KB per GPU)
+constexpr int kEulerScratchPartials = 16384;
 struct EulerArgs {
     const void* x;
     const void* v_pos;
@@ -230,6 +233,9 @@ hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, 
 hipError_t launch_gemm_residual(GemmArgs a, hipStream_t s);
 // t2h_sampler.hip
 hipError_t launch_euler(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, hipStream_t s);
+// Device address of the current device's built-in statistics scratch
+// (kEulerScratchPartials f64 quads), looked up once per device.
+hipError_t euler_scratch(double** out);
 // t2h_eltwise.hip
 hipError_t launch_activation(const EltArgs& a, hipStream_t s);
 hipError_t launch_gate_residual(const EltArgs& a, hipStream_t s);

@@ -35,6 +35,9 @@
 // Reference: samplers/flow_euler.mojo:56-57 (_scaled), 68-70
 // (_v_to_xstart), 75-149 (_rescale_pred), 151-181 (_inference),
 // 196-210 (_sample_impl step).
+#include <mutex>
+#include <vector>
+
 #include "t2h_device.h"
 #include "t2h_internal.h"
 
@@ -330,7 +333,38 @@ hipError_t launch_typed(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, 
     return hipGetLastError();
 }
 
+// The built-in statistics scratch of t2h_flow_euler_step_noalloc: f64
+// partial quads for up to kEulerScratchPartials statistics blocks (512 KB),
+// one copy per GPU at its own address, held until the process ends. Host
+// code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): euler_scratch() looks the device address
+// up with hipGetSymbolAddress once per device and every launch takes that.
+// Every statistics block writes its quad before the elementwise pass reads
+// it, so nothing has to start at zero; calls that overlap on one GPU share
+// the array and race.
+__device__ __align__(256) double scratch[kEulerScratchPartials * 4];
+
 }  // namespace
+
+hipError_t euler_scratch(double** out) {
+    static std::mutex mu;
+    static std::vector<double*> ptrs;   // per device ordinal
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(mu);
+    if (dev < (int)ptrs.size() && ptrs[dev] != nullptr) {
+        *out = ptrs[dev];
+        return hipSuccess;
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));   // with `dev` current
+    if (e != hipSuccess) return e;
+    if (dev >= (int)ptrs.size()) ptrs.resize(dev + 1, nullptr);
+    ptrs[dev] = static_cast<double*>(p);
+    *out = ptrs[dev];
+    return hipSuccess;
+}
 
 hipError_t launch_euler(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, hipStream_t s) {
     switch (a.dtype) {

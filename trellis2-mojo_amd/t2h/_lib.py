@@ -52,6 +52,8 @@ _SIGNATURES = {
     "t2h_modulation_add": [c_p, c_p, c_p, c_i64, c_i64, c_p],
     "t2h_flow_euler_step": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_f64, c_f64, c_f64, c_f64, c_f64, c_p,
                             c_i32, c_p, c_i64, c_p],
+    "t2h_flow_euler_step_noalloc": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_f64, c_f64, c_f64, c_f64, c_f64,
+                                    c_p, c_i32, c_p],
     "t2h_ln_mod_rows": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p],
     "t2h_gate_add_bias_rows": [c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_p],
     "t2h_block_join_ln": [c_p, c_p, c_p, c_p, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_p],
