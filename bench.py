@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
-    p.add_argument("--all-configs", action="store_true", help="also time BASELINE configs 1-4 (stderr)")
+    p.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1-4")
     p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
     return p.parse_args()
 
@@ -260,99 +260,258 @@ def time_op(torch, fn, reps, flush=None):
     return statistics.median(times)
 
 
+def cpu_info():
+    """nproc, the CPUs this process may run on, and the CPU model."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"nproc": os.cpu_count() or 1, "usable_cpus": usable, "cpu_model": model}
+
+
 def cpu_baseline(chain, target_s):
-    """The C oracle (the reference's CPU path restated; serial LN/modulate/
-    phase build/gate, OpenMP GELU/RMSNorm/rotate chunks) over a bounded sample
-    of the same chain: f32 math on the f16-rounded inputs of the first
-    `n` tokens; n grows until one pass takes about target_s."""
+    """The C oracle (the reference's CPU path restated) over the config-5
+    chain, f32 math on the f16-rounded inputs of the first n tokens (n grows
+    until one pass takes about target_s), timed two ways on the host cores:
+    - "reference threading": LN/modulate, the phase build and the gated
+      residual serial, GELU/RMSNorm/RoPE-rotate in OpenMP chunks above 2^17
+      elements, as the reference's parallelize calls;
+    - "all cores": every op split by rows over the same threads (ctypes
+      releases the GIL, so the C oracle runs in parallel).
+    Threads = the CPUs this process may use, at most 16 (the box's CPU share
+    for one GPU)."""
+    import concurrent.futures as cf
+
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
 
-    torch = chain.torch
-    threads = min(os.cpu_count() or 1, 16)
-    C, H, D, F = chain.C, chain.H, chain.D, chain.F
+    info = cpu_info()
+    threads = max(1, min(info["usable_cpus"], 16))
+    D = chain.D
+    pool = cf.ThreadPoolExecutor(threads)
 
-    def run(n):
-        x = chain.x[:n].float().cpu().numpy()
-        q, k = chain.q[:n].float().cpu().numpy(), chain.k[:n].float().cpu().numpy()
-        u, y = chain.u[:n].float().cpu().numpy(), chain.y[:n].float().cpu().numpy()
-        co = chain.coords_np[:n]
-        sh, sc, gt = (a.cpu().numpy() for a in (chain.shift, chain.scale, chain.gate))
-        gq, gk, bias = chain.gq.cpu().numpy(), chain.gk.cpu().numpy(), chain.bias.cpu().numpy()
-        tt = chain.t.cpu().numpy()
+    def inputs(n):
+        d = {"x": chain.x[:n].float().cpu().numpy(), "q": chain.q[:n].float().cpu().numpy(),
+             "k": chain.k[:n].float().cpu().numpy(), "u": chain.u[:n].float().cpu().numpy(),
+             "y": chain.y[:n].float().cpu().numpy(), "co": chain.coords_np[:n]}
+        d.update(sh=chain.shift.cpu().numpy(), sc=chain.scale.cpu().numpy(), gt=chain.gate.cpu().numpy(),
+                 gq=chain.gq.cpu().numpy(), gk=chain.gk.cpu().numpy(), bias=chain.bias.cpu().numpy(),
+                 tt=chain.t.cpu().numpy(), freqs=orc.rope_freqs(D))
+        return d
+
+    def run_reference(d, n):
         off = np.array([0, n], np.int64)
-        freqs = orc.rope_freqs(D)
         t0 = time.perf_counter()
-        orc.timestep_embedding(tt, 256)
-        orc.ln_modulate(x, sh, sc, offsets=off, eps=1e-6)
-        ph = orc.rope_phases_from_coords(co, D, freqs)
-        orc.qk_rms_rope(q, k, gq, gk, ph, nthreads=threads)
-        orc.gelu_tanh_bias(u, bias, nthreads=threads)
-        orc.gate_residual(x, y, gt, offsets=off)
+        orc.timestep_embedding(d["tt"], 256)
+        orc.ln_modulate(d["x"], d["sh"], d["sc"], offsets=off, eps=1e-6)
+        ph = orc.rope_phases_from_coords(d["co"], D, d["freqs"])
+        orc.qk_rms_rope(d["q"], d["k"], d["gq"], d["gk"], ph, nthreads=threads)
+        orc.gelu_tanh_bias(d["u"], d["bias"], nthreads=threads)
+        orc.gate_residual(d["x"], d["y"], d["gt"], offsets=off)
         return time.perf_counter() - t0
 
-    n = 2048
-    dt = run(n)
-    n = int(min(chain.T, max(n, n * target_s / max(dt, 1e-3))))
-    dt = run(n)
-    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"one pass of the config-5 chain over the first {n} of {chain.T} tokens "
-                      f"(f32 C oracle on f16-rounded inputs, {dt:.1f} s; OpenMP {threads} threads for "
-                      f"GELU/RMSNorm/RoPE-rotate as the reference's parallelize, the rest serial)",
-            "seconds": dt, "tokens": n, "gbs_equiv": chain.chain_bytes / chain.T * n / dt / 1e9}
+    def run_all_cores(d, n):
+        cuts = np.linspace(0, n, threads + 1).astype(np.int64)
+        parts = list(zip(cuts[:-1], cuts[1:]))
+
+        def piece(lo, hi):
+            m = hi - lo
+            off = np.array([0, m], np.int64)
+            orc.ln_modulate(d["x"][lo:hi], d["sh"], d["sc"], offsets=off, eps=1e-6)
+            ph = orc.rope_phases_from_coords(d["co"][lo:hi], D, d["freqs"])
+            orc.qk_rms_rope(d["q"][lo:hi], d["k"][lo:hi], d["gq"], d["gk"], ph, nthreads=1)
+            orc.gelu_tanh_bias(d["u"][lo:hi], d["bias"], nthreads=1)
+            orc.gate_residual(d["x"][lo:hi], d["y"][lo:hi], d["gt"], offsets=off)
+
+        t0 = time.perf_counter()
+        orc.timestep_embedding(d["tt"], 256)
+        list(pool.map(lambda p: piece(*p), parts))
+        return time.perf_counter() - t0
+
+    out = {}
+    for name, fn in (("reference_threading", run_reference), ("all_cores", run_all_cores)):
+        n = 2048
+        dt = fn(inputs(n), n)
+        n = int(min(chain.T, max(n, n * target_s / max(dt, 1e-3))))
+        dt = fn(inputs(n), n)
+        out[name] = {"tokens_per_s": n / dt, "seconds": dt, "tokens": n,
+                     "gbs_equiv": chain.chain_bytes / chain.T * n / dt / 1e9}
+    pool.shutdown()
+    ref = out["reference_threading"]
+    n = ref["tokens"]
+    return {"value": ref["tokens_per_s"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one pass of the config-5 chain over the first {n} of {chain.T} tokens (f32 C oracle on "
+                      f"f16-rounded inputs, {ref['seconds']:.1f} s) with the reference's threading: OpenMP "
+                      f"{threads} threads for GELU/RMSNorm/RoPE-rotate as its parallelize, the rest serial",
+            "all_cores": {"value": out["all_cores"]["tokens_per_s"], "threads": threads,
+                          "seconds": out["all_cores"]["seconds"], "tokens": out["all_cores"]["tokens"],
+                          "note": "every op split by rows over the same threads"},
+            **info, "gbs_equiv": ref["gbs_equiv"]}
 
 
-def other_configs(torch, dev):
-    """BASELINE configs 1-4, each op alone, warm and cold (caches flushed)."""
+def other_configs(torch, dev, cpu=True):
+    """BASELINE configs 1-4, each op alone: GPU warm and cold (caches flushed
+    by a 1 GiB fill before each launch), and the C oracle on the same inputs
+    on the host (the reference's threading: LN/modulate/gate serial, GELU,
+    RMSNorm and RoPE-rotate in OpenMP chunks; best of 2 passes)."""
     import numpy as np
 
     from t2h import nn, ops, workloads
 
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    threads = max(1, min(cpu_info()["usable_cpus"], 16))
     g = torch.Generator(device=dev).manual_seed(1)
     rn = lambda shape, std=1.0, mean=0.0, dt=torch.float32: (
         torch.randn(shape, generator=g, device=dev) * std + mean).to(dt)
+    hst = lambda t: t.float().cpu().numpy()
     flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     flush = lambda: flush_buf.zero_()
     res = {}
 
-    def rec(name, fn, nbytes, tokens, reps=30):
+    def rec(name, fn, nbytes, tokens, cpu_fn, reps=30):
         for _ in range(3):
             fn()
         warm = time_op(torch, fn, reps)
         cold = time_op(torch, fn, reps, flush)
-        res[name] = {"bytes": nbytes, "tokens": tokens, "warm_ms": warm, "cold_ms": cold,
-                     "warm_gbs": nbytes / warm / 1e6, "cold_gbs": nbytes / cold / 1e6,
-                     "cold_pct_peak": nbytes / cold / 1e6 / HBM_PEAK_GBS * 100,
-                     "tokens_per_s_cold": tokens / cold * 1e3}
+        r = {"bytes": nbytes, "tokens": tokens, "warm_us": round(warm * 1e3, 2), "cold_us": round(cold * 1e3, 2),
+             "warm_gbs": round(nbytes / warm / 1e6, 1), "cold_gbs": round(nbytes / cold / 1e6, 1),
+             "cold_pct_peak": round(nbytes / cold / 1e6 / HBM_PEAK_GBS * 100, 2),
+             "warm_pct_peak": round(nbytes / warm / 1e6 / HBM_PEAK_GBS * 100, 2),
+             "tokens_per_s_cold": round(tokens / cold * 1e3), "tokens_per_s_warm": round(tokens / warm * 1e3)}
+        msg = ""
+        if cpu and cpu_fn is not None:
+            best = None
+            for _ in range(2):
+                t0 = time.perf_counter()
+                cpu_fn()
+                dt = time.perf_counter() - t0
+                best = dt if best is None else min(best, dt)
+            r["cpu_tokens_per_s"] = round(tokens / best)
+            r["cpu_threads"] = threads
+            msg = f" | cpu {tokens / best:10.0f} tok/s"
+        res[name] = r
         log(f"  {name:<28s} warm {warm*1e3:8.1f} us {nbytes/warm/1e6:8.1f} GB/s | cold {cold*1e3:8.1f} us "
-            f"{nbytes/cold/1e6:8.1f} GB/s ({nbytes/cold/1e6/HBM_PEAK_GBS*100:5.1f}%)")
+            f"{nbytes/cold/1e6:8.1f} GB/s ({nbytes/cold/1e6/HBM_PEAK_GBS*100:5.1f}%){msg}")
 
     C = 1536
     x = rn((4096, C)); sh = rn((C,), 0.1); sc = rn((C,), 0.1); out = torch.empty_like(x)
-    rec("c1_ln_modulate_f32", lambda: ops.ln_modulate(x, 1e-6, shift=sh, scale=sc, out=out), 2 * 4096 * C * 4 + 2 * C * 4, 4096)
+    hx, hsh, hsc = hst(x), hst(sh), hst(sc)
+    rec("c1_ln_modulate_f32", lambda: ops.ln_modulate(x, 1e-6, shift=sh, scale=sc, out=out),
+        2 * 4096 * C * 4 + 2 * C * 4, 4096, lambda: orc.ln_modulate(hx, hsh, hsc, eps=1e-6))
     q, k = rn((4096, 12, 128)), rn((4096, 12, 128)); gq, gk = rn((12, 128), 0.02, 1.0), rn((12, 128), 0.02, 1.0)
     qo, ko = torch.empty_like(q), torch.empty_like(k); fr = nn.rope_freqs(128)
+    hq, hk, hgq, hgk = hst(q), hst(k), hst(gq), hst(gk)
+    ofr = orc.rope_freqs(128)
+
+    def cpu_c2():   # phases built per forward from the grid (modules/rope.mojo:39-61), then RMS + rotate
+        ph = orc.rope_phases_from_positions(orc.grid_positions(16), 128, ofr)
+        orc.qk_rms_rope(hq, hk, hgq, hgk, ph, nthreads=threads)
+
     rec("c2_qk_rms_rope_f32", lambda: ops.qk_rmsnorm_rope(q=q, k=k, gamma_q=gq, gamma_k=gk, freqs=fr, grid_res=16,
-                                                           q_out=qo, k_out=ko), 4 * 4096 * C * 4 + 2 * C * 4, 4096)
+                                                           q_out=qo, k_out=ko), 4 * 4096 * C * 4 + 2 * C * 4, 4096,
+        cpu_c2)
     del x, out, q, k, qo, ko
     h = rn((32768, 6144), dt=torch.float16); b = rn((6144,), 0.02); ho = torch.empty_like(h)
-    rec("c3a_gelu_bias_f16", lambda: ops.activation(h, 3, bias=b, out=ho), 2 * 32768 * 6144 * 2 + 6144 * 4, 32768, 20)
-    del h, ho
+    hh, hb = hst(h), hst(b)
+    rec("c3a_gelu_bias_f16", lambda: ops.activation(h, 3, bias=b, out=ho), 2 * 32768 * 6144 * 2 + 6144 * 4, 32768,
+        lambda: orc.gelu_tanh_bias(hh, hb, nthreads=threads), 20)
+    del h, ho, hh
     xr, yr = rn((32768, C), dt=torch.float16), rn((32768, C), dt=torch.float16); gt = rn((C,), 0.1)
     ro = torch.empty_like(xr)
-    rec("c3b_gated_residual_f16", lambda: ops.gate_residual(xr, yr, gate=gt, out=ro), 3 * 32768 * C * 2 + C * 4, 32768)
-    del xr, yr, ro
+    hxr, hyr, hgt = hst(xr), hst(yr), hst(gt)
+    rec("c3b_gated_residual_f16", lambda: ops.gate_residual(xr, yr, gate=gt, out=ro), 3 * 32768 * C * 2 + C * 4,
+        32768, lambda: orc.gate_residual(hxr, hyr, hgt))
+    del xr, yr, ro, hxr, hyr
     coords, offsets = workloads.config4()
     T = coords.shape[0]
     co, off = torch.from_numpy(coords).to(dev), torch.from_numpy(offsets).to(dev)
     f4 = rn((T, C)); s4, c4 = rn((2, C), 0.1), rn((2, C), 0.1); o4 = torch.empty_like(f4)
+    hf4, hs4, hc4 = hst(f4), hst(s4), hst(c4)
     rec("c4_sparse_ln_mod_f32", lambda: ops.ln_modulate(f4, 1e-6, shift=s4, scale=c4, offsets=off, out=o4),
-        2 * T * C * 4 + 2 * 2 * C * 4 + 16, T)
+        2 * T * C * 4 + 2 * 2 * C * 4 + 16, T, lambda: orc.ln_modulate(hf4, hs4, hc4, offsets=offsets, eps=1e-6))
     q4, k4 = rn((T, 12, 128)), rn((T, 12, 128)); q4o, k4o = torch.empty_like(q4), torch.empty_like(k4)
+    hq4, hk4 = hst(q4), hst(k4)
+
+    def cpu_c4():   # phases from the int coords (sparse/attention/rope.mojo:48-66), then RMS + rotate
+        ph = orc.rope_phases_from_coords(coords, 128, ofr)
+        orc.qk_rms_rope(hq4, hk4, hgq, hgk, ph, nthreads=threads)
+
     rec("c4_sparse_qk_rope_f32", lambda: ops.qk_rmsnorm_rope(q=q4, k=k4, gamma_q=gq, gamma_k=gk, freqs=fr, coords=co,
-                                                              q_out=q4o, k_out=k4o), 4 * T * C * 4 + T * 16, T)
+                                                              q_out=q4o, k_out=k4o), 4 * T * C * 4 + T * 16, T,
+        cpu_c4)
+    return res
+
+
+def small_t_block(torch, dev, reps):
+    """The dense sparse-structure DiT's block at its real shape: 4096 tokens
+    (16^3 grid), width 1536, 12 x 128 heads, hidden 6144, f32 (the
+    reference's dtype; models/sparse_structure_flow.mojo:190-206 runs it 30
+    blocks x 2 CFG branches x the sampler steps). One block's per-token work
+    over the 12*C const buffer (gpu/block.mojo:217-397), the GEMM and SDPA
+    outputs stubbed by resident tensors:
+      LN1 + modulate -> qkv epilogue in place (bias, RMS q/k, RoPE from the
+      grid) -> self join + norm2 (affine) -> cross join + LN3 + modulate ->
+      GELU-tanh + bias on the MLP hidden -> gated MLP join.
+    Timed as eager launches and as one HIP-graph replay per block."""
+    from t2h import block, nn, ops
+
+    T, C, H, D, F = 4096, 1536, 12, 128, 6144
+    g = torch.Generator(device=dev).manual_seed(11)
+    rn = lambda shape, std=1.0, mean=0.0: torch.randn(shape, generator=g, device=dev) * std + mean
+    m = [rn((C,), 0.1) for _ in range(6)]
+    bk = block.pack_block_consts(m, rn((C,), 0.1, 1.0), rn((C,), 0.1), rn((C,), 0.02), rn((C,), 0.02),
+                                 rn((C,), 0.02))
+    x0 = rn((T, C))
+    x, hs, hs2 = x0.clone(), torch.empty(T, C, device=dev), torch.empty(T, C, device=dev)
+    qkv, h_self, h_cross, hid, h_mlp = rn((T, 3 * C)), rn((T, C)), rn((T, C)), rn((T, F)), rn((T, C))
+    hid_out = torch.empty_like(hid)
+    qkv_bias, fbias = rn((3 * C,), 0.02), rn((F,), 0.02)
+    gq, gk = rn((H, D), 0.02, 1.0), rn((H, D), 0.02, 1.0)
+    freqs = nn.rope_freqs(D)
+
+    def step():
+        ops.ln_mod_rows(x, hs, bk, 0, 1)
+        ops.qkv_bias_rmsnorm_rope(qkv, H, D, bias=qkv_bias, gamma_q=gq, gamma_k=gk, freqs=freqs, grid_res=16)
+        ops.block_join_ln(x, h_self, hs2, bk, 2 * C, 1, 4 * C, 2)
+        ops.block_join_ln(x, h_cross, hs, bk, 6 * C, 0, 8 * C, 1)
+        ops.activation(hid, ops.ACT_GELU_TANH, bias=fbias, out=hid_out)
+        ops.gate_add_bias_rows(x, h_mlp, bk, 10 * C, 1)
+
+    e = 4
+    nbytes = (2 + 6 + 4 + 4 + 3) * T * C * e + 2 * T * F * e + 12 * C * 4
+    step()
+    eager = time_region(torch, step, reps) / reps
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph.replay()
+    replay = time_region(torch, graph.replay, reps) / reps
+    res = {"tokens": T, "launches": 6, "bytes": nbytes,
+           "eager_us": round(eager * 1e3, 2), "graph_us": round(replay * 1e3, 2),
+           "eager_gbs": round(nbytes / eager / 1e6, 1), "graph_gbs": round(nbytes / replay / 1e6, 1),
+           "graph_pct_peak": round(nbytes / replay / 1e6 / HBM_PEAK_GBS * 100, 2)}
+    log(f"  ss-flow block glue + qk f32 [4096]: eager {eager*1e3:.1f} us ({nbytes/eager/1e6:.0f} GB/s), "
+        f"graph replay {replay*1e3:.1f} us ({nbytes/replay/1e6:.0f} GB/s)")
+    del graph
     return res
 
 
@@ -504,13 +663,17 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(chain, args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']:.0f} tokens/s on {cpu['cores']} threads ({cpu['sample']})")
+        log(f"cpu baseline: {cpu['value']:.0f} tokens/s on {cpu['cores']} threads ({cpu['sample']}); all cores "
+            f"{cpu['all_cores']['value']:.0f} tokens/s; nproc {cpu['nproc']}, usable {cpu['usable_cpus']}, "
+            f"{cpu['cpu_model']}")
     log("next rows on the config-5 rows (f16):")
     extra = next_rows(torch, dev, chain, max(10, args.steps))
-    if args.all_configs:
+    log("small-T block (dense sparse-structure DiT, 4096 tokens):")
+    small = small_t_block(torch, dev, max(20, args.steps))
+    other = None
+    if not args.no_configs:
         log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
         other = other_configs(torch, dev)
-        log("configs 1-4 as JSON: " + json.dumps(other))
 
     out = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -525,7 +688,11 @@ def main():
         "per_op": {k: {"us": round(v["us"], 2), "gbs": round(v["gbs"], 1)} for k, v in per_op.items()},
         "next_rows": extra,
         "roofline": roofline,
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                                                      "all_cores", "nproc", "usable_cpus",
+                                                                      "cpu_model")},
+        "configs": other,
+        "small_t_block": small,
     }
     print(json.dumps(out), flush=True)
 
