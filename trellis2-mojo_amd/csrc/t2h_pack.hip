@@ -34,7 +34,10 @@
 namespace t2h {
 namespace {
 
-constexpr int kPackRows = 64;
+#ifndef T2H_PACK_ROWS
+#define T2H_PACK_ROWS 64
+#endif
+constexpr int kPackRows = T2H_PACK_ROWS;   // token rows per tile block
 constexpr int kPackBlock = 256;
 constexpr int kPackIters = kPackRows / 16;   // row groups of 4 per wave
 
