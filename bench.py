@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
     p.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1-4")
     p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
+    p.add_argument("--probe", action="store_true",
+                   help="time the HBM streaming probes (lib/libhbm_probe.so) instead of the chain")
     return p.parse_args()
 
 
@@ -651,6 +653,36 @@ def next_rows(torch, dev, chain, reps):
     return res
 
 
+def hbm_probes(torch, dev, steps):
+    """The streaming probes of trellis2-mojo_amd/probe/hbm_probe.hip on the
+    config-5 GELU tensor (f16 [201436, 6144]): what each access pattern and
+    block shape reaches with nothing else in the kernel. Prints one JSON line."""
+    import ctypes
+
+    from t2h import _build
+
+    L = ctypes.CDLL(_build.PROBE_PATH)
+    L.hbm_probe_name.restype = ctypes.c_char_p
+    L.hbm_probe_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                   ctypes.c_void_p]
+    rows, cols = 201436, 6144
+    g = torch.Generator(device=dev).manual_seed(3)
+    src = torch.randn((rows, cols), generator=g, device=dev).half()
+    dst = torch.empty_like(src)
+    bias = torch.randn((cols,), generator=g, device=dev) * 0.02
+    st = torch.cuda.current_stream().cuda_stream
+    nbytes = 2 * rows * cols * 2
+    res = {}
+    for i in range(L.hbm_probe_count()):
+        name = L.hbm_probe_name(i).decode()
+        fn = lambda: L.hbm_probe_launch(i, src.data_ptr(), dst.data_ptr(), bias.data_ptr(), rows, st)
+        assert fn() == 0, name
+        ms = time_region(torch, fn, steps) / steps
+        res[name] = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / ms / 1e6, 1)}
+        log(f"  {name:<20s} {ms*1e3:8.1f} us {nbytes/ms/1e6:8.1f} GB/s ({nbytes/ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
+    print(json.dumps({"hbm_probes": res, "bytes_per_launch": nbytes}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -665,6 +697,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     ops.device_init(0)
+    if args.probe:
+        hbm_probes(torch, dev, args.steps)
+        return
     dtype = torch.float16
     chain = Chain(dev, dtype)
     log(f"config5: T={chain.T} tokens, chain bytes {chain.chain_bytes/1e9:.3f} GB/step")

@@ -247,4 +247,19 @@ __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 // dimension only past 2^20 blocks; see t2h_internal.h).
 __device__ __forceinline__ int64_t block_linear() { return (int64_t)blockIdx.y * gridDim.x + blockIdx.x; }
 
+// Block order over T2H_FRONTS contiguous ranges ("fronts"): physical block
+// b runs logical block (b % P) * per + b / P, so P fronts of consecutive
+// logical blocks stream at once (front f on XCD f % 8). P = 1: identity.
+#ifndef T2H_FRONTS
+#define T2H_FRONTS 1
+#endif
+__device__ __forceinline__ int64_t front_of(int64_t b, int64_t per) {
+    if constexpr (T2H_FRONTS == 1) {
+        (void)per;
+        return b;
+    } else {
+        return (b % T2H_FRONTS) * per + b / T2H_FRONTS;
+    }
+}
+
 }  // namespace t2h

@@ -65,7 +65,7 @@ struct Tile {
 // from the host: no 64-bit division per wave, none at all for row-wide blocks.
 template <int V>
 __device__ __forceinline__ bool tile_of(const EltArgs& a, Tile& t) {
-    const int64_t b = block_linear();
+    const int64_t b = front_of(block_linear(), a.fper);
     int64_t rt, cb;
     if (a.col_tiles == 1) {
         rt = b;
@@ -330,7 +330,8 @@ hipError_t tile_launch(K kernel, EltArgs a, hipStream_t s) {
     const int64_t rt = (a.rows + kRpt - 1) / kRpt;
     const int64_t ct = (a.cols + bw - 1) / bw;
     a.col_tiles = (int32_t)ct;
-    hipLaunchKernelGGL(kernel, grid_1d(rt * ct), dim3(tile_block<V>(a)), 0, s, a);
+    a.fper = front_per(rt * ct);
+    hipLaunchKernelGGL(kernel, grid_1d(front_grid(rt * ct)), dim3(tile_block<V>(a)), 0, s, a);
     return hipGetLastError();
 }
 

@@ -8,6 +8,10 @@
 
 #include "t2h.h"
 
+#ifndef T2H_FRONTS
+#define T2H_FRONTS 1   // block order over contiguous fronts (front_of in t2h_device.h)
+#endif
+
 namespace t2h {
 
 struct BatchArgs {
@@ -33,6 +37,7 @@ struct LnArgs {
     int32_t cols;
     int32_t dtype;
     BatchArgs batch;
+    int64_t fper;        // logical blocks per front (set at launch)
 };
 
 // Per-slot RoPE table, passed by value as a kernel argument: slot p rotates
@@ -68,6 +73,7 @@ struct QkArgs {
     const int32_t* coords;   // position source 2
     int32_t coord_cols;
     int32_t grid_res;        // position source 3
+    int64_t fper;            // logical tiles per front (set at launch)
 };
 
 // Self-attention epilogue + head-major packing (t2h_attn_pack).
@@ -206,6 +212,7 @@ struct EltArgs {
     int32_t kind;          // activation kind / binop op
     BatchArgs batch;
     int32_t col_tiles;     // row-tiled kernels: blocks across one row (set at launch)
+    int64_t fper;          // logical blocks per front (set at launch)
 };
 
 // Grid of nblocks blocks. A dispatch counts work-items in 32 bits per grid
@@ -217,6 +224,11 @@ inline dim3 grid_1d(int64_t nblocks) {
     if (nblocks <= kGridX) return dim3((unsigned)nblocks);
     return dim3((unsigned)kGridX, (unsigned)((nblocks + kGridX - 1) / kGridX));
 }
+// Logical blocks per front and the physical block count of a launch in
+// T2H_FRONTS fronts (front_of() in t2h_device.h); kernels return on logical
+// blocks past their last one.
+inline int64_t front_per(int64_t nblocks) { return (nblocks + T2H_FRONTS - 1) / T2H_FRONTS; }
+inline int64_t front_grid(int64_t nblocks) { return front_per(nblocks) * T2H_FRONTS; }
 
 // t2h_norm.hip
 hipError_t launch_ln(const LnArgs& a, hipStream_t s);

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
     __shared__ __attribute__((aligned(16))) float ps[NP * C];
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t r0 = block_linear() * kWavesPerBlock;
+    const int64_t r0 = front_of(block_linear(), a.fper) * kWavesPerBlock;
     if (r0 >= a.rows) return;   // past the last row of a 2-D grid (block-uniform)
     const int64_t r = r0 + wave;
     const bool live = r < a.rows;
@@ -247,9 +247,10 @@ int resident_blocks(K kernel) {
 }
 
 template <typename T, int NCH, bool JOIN>
-hipError_t launch_fast(const LnArgs& a, hipStream_t s) {
+hipError_t launch_fast(LnArgs a, hipStream_t s) {
     const int64_t grid = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
-    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), grid_1d(grid), dim3(kFastBlock), 0, s, a);
+    a.fper = front_per(grid);
+    hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), grid_1d(front_grid(grid)), dim3(kFastBlock), 0, s, a);
     return hipGetLastError();
 }
 

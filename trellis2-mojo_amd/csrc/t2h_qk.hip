@@ -58,7 +58,7 @@ __global__ __launch_bounds__(kTileBlock) void qk_tile_kernel(QkArgs a, RopeSlots
     int which = (int)(b % upr);   // 0 = q, 1 = k, 2 = v (absent tensors skipped)
     if (!has_q) ++which;
     if (which == 1 && !has_k) ++which;
-    const int64_t tile = b / upr;
+    const int64_t tile = front_of(b / upr, a.fper);
     if (tile * kTileWaves >= a.rows) return;   // past the last tile of a 2-D grid (block-uniform)
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t r = tile * kTileWaves + wave;
@@ -278,10 +278,12 @@ int resident_blocks(K kernel) {
 }
 
 template <typename T, int D, int NG>
-hipError_t launch_fast(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
+hipError_t launch_fast(QkArgs a, const RopeSlots& tab, hipStream_t s) {
     const int upr = (a.q_in != nullptr) + (a.k_in != nullptr) + (a.v != nullptr && a.bias_v != nullptr);
     const int64_t tiles = (a.rows + kTileWaves - 1) / kTileWaves;
-    hipLaunchKernelGGL((qk_tile_kernel<T, D, NG>), grid_1d(tiles * upr), dim3(kTileBlock), 0, s, a, tab);
+    a.fper = front_per(tiles);
+    hipLaunchKernelGGL((qk_tile_kernel<T, D, NG>), grid_1d(front_grid(tiles) * upr), dim3(kTileBlock), 0, s, a,
+                       tab);
     return hipGetLastError();
 }
 
