@@ -616,3 +616,59 @@ def test_linear_float64_bound_bias_and_activation():
     assert np.max(np.abs(got - exact)) > 0.0      # f32 sums do round
     full = orc.linear(a, w, bias=b, act=orc.ACT_GELU_TANH)
     assert np.array_equal(full, orc.activation(orc.add_bias(got, b), orc.ACT_GELU_TANH))
+
+
+# ---- compositions the GPU tests check against -------------------------------
+def test_compositions_float64_and_order():
+    """The oracle's compositions follow the reference's op order, checked in
+    float64 against closed forms of the same order; each plausible reordering
+    (RoPE before RMS with a non-uniform gamma, the bias after RMS, GELU of x
+    then + bias, modulate before LN) fails the same check.
+    - qk_rms_rope: bias -> MultiHeadRMSNorm -> RoPE (sparse/attention/
+      modules.mojo:206-212; gpu/attention.mojo:507-563);
+    - ln_modulate: LN then x*(1+scale)+shift (modules/nn.mojo:660-689);
+    - gelu_tanh_bias: GELU-tanh(x + bias) (gpu/linear.mojo:662-684);
+    - attn_pack: the epilogue, then pack_q_z / pack_kv_z (987-1013)."""
+    n, h, d = 24, 4, 64
+    q = orc.randn(2200, (n, h, d), std=2.0)
+    k = orc.randn(2201, (n, h, d), std=2.0)
+    g = orc.randn(2202, (h, d), mean=1.0, std=0.3)       # non-uniform: RMS and RoPE do not commute
+    bq = orc.randn(2203, (h, d), std=0.5)
+    co = np.zeros((n, 4), np.int32)
+    co[:, 1:] = np.random.default_rng(3).integers(0, 40, (n, 3))
+    ph = orc.rope_phases_from_coords(co, d, orc.rope_freqs(d))
+    ph64 = ph.astype(np.float64)[:, None]
+
+    def rms64(x, gam):
+        x = x.astype(np.float64)
+        return x / np.maximum(np.linalg.norm(x, axis=-1, keepdims=True), 1e-12) * gam * math.sqrt(d)
+
+    want = _rotate64(rms64(q + bq, g).astype(np.float32), ph64)
+    got_q, _ = orc.qk_rms_rope(q, k, g, g, ph, bias_q=bq)
+    assert _rel(got_q, want) < 5e-6
+    assert _rel(rms64(_rotate64(q + bq, ph64), g), want) > 1e-3            # RoPE before RMS
+    assert _rel(_rotate64(rms64(q, g) + bq, ph64), want) > 1e-3            # bias after RMS
+
+    x = orc.randn(2204, (16, 96), mean=0.3, std=1.7)
+    sh, sc = orc.randn(2205, (96,), std=0.3), orc.randn(2206, (96,), std=0.3)
+    ln = _ln64(x, 1e-6)
+    want = ln * (1.0 + sc.astype(np.float64)) + sh
+    assert _rel(orc.ln_modulate(x, sh, sc, eps=1e-6), want) < 2e-6
+    assert _rel(_ln64((x * (1.0 + sc) + sh).astype(np.float32), 1e-6), want) > 1e-3   # modulate first
+
+    u = orc.randn(2207, (8, 300), std=2.0)
+    b = orc.randn(2208, (300,), std=0.5)
+    gelu64 = lambda v: 0.5 * v * (1.0 + np.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
+    want = gelu64(u.astype(np.float64) + b)
+    assert _rel(orc.gelu_tanh_bias(u, b), want) < 2e-6
+    assert _rel(gelu64(u.astype(np.float64)) + b, want) > 1e-3                       # bias after GELU
+
+    qkv = orc.randn(2209, (n, 3, h, d))
+    bias = orc.randn(2210, (3, h, d), std=0.5)
+    qh, kt, vh = orc.attn_pack(qkv, h, d, 32, 32, bias.reshape(-1), g, g, ph)
+    eq, ek = orc.qk_rms_rope(qkv[:, 0], qkv[:, 1], g, g, ph, bias_q=bias[0], bias_k=bias[1])
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    assert np.array_equal(qh[:, :n], (eq * scale).astype(np.float32).transpose(1, 0, 2))
+    assert np.array_equal(kt[:, :, :n], ek.transpose(1, 2, 0))
+    assert np.array_equal(vh[:, :n], (qkv[:, 2] + bias[2]).astype(np.float32).transpose(1, 0, 2))
+    assert not qh[:, n:].any() and not kt[:, :, n:].any() and not vh[:, n:].any()
