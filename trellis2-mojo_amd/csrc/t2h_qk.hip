@@ -35,7 +35,10 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 
-constexpr int kTileWaves = 8;
+#ifndef T2H_QK_WAVES
+#define T2H_QK_WAVES 8
+#endif
+constexpr int kTileWaves = T2H_QK_WAVES;   // token rows (one per wave) per tile block
 constexpr int kTileBlock = kTileWaves * 64;
 
 template <typename T, int D, int NG>
