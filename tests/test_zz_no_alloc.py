@@ -75,3 +75,35 @@ def test_noalloc_rejects_states_beyond_its_scratch(dev):
     got = _noalloc(x, vp, vn, 0.8, 0.7, 3.0, 0.5, None)
     want = ops.flow_euler_step(x, vp, 0.8, 0.7, SM, v_neg=vn, guidance_strength=3.0, guidance_rescale=0.5)
     assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+def test_noalloc_step_in_a_hip_graph(dev):
+    """The entry point's purpose: a sampler step recorded into a HIP graph.
+    t2h_device_init did the scratch lookup, so the call only enqueues its
+    kernels. Three replays with fresh inputs, eager no-allocation calls in
+    between (which reuse the same scratch), each equal to the workspace entry
+    point's result bit for bit."""
+    _, off4 = workloads.config4()
+    segs = off4.tolist()
+    x, vp, vn = _state(4040, (int(off4[-1]), 32), dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _noalloc(x, vp, vn, 0.8, 0.7, 3.0, 0.5, segs)          # warm-up off the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = _noalloc(x, vp, vn, 0.8, 0.7, 3.0, 0.5, segs)
+    g = torch.Generator(device=dev).manual_seed(4041)
+    for rep in range(3):
+        for a in (x, vp, vn):
+            a.copy_(torch.randn(a.shape, generator=g, device=dev))
+        graph.replay()
+        other = _noalloc(vn, x, vp, 0.6, 0.5, 2.0, 0.7, segs)   # an eager call on the same scratch
+        want = ops.flow_euler_step(x, vp, 0.8, 0.7, SM, v_neg=vn, guidance_strength=3.0, guidance_rescale=0.5,
+                                   seg_offsets=segs)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], want[0]) and torch.equal(outs[1], want[1]), f"replay {rep}"
+        ref_other = ops.flow_euler_step(vn, x, 0.6, 0.5, SM, v_neg=vp, guidance_strength=2.0, guidance_rescale=0.7,
+                                        seg_offsets=segs)
+        assert torch.equal(other[0], ref_other[0]), f"eager call after replay {rep}"
