@@ -1,0 +1,663 @@
+// t2h.hpp — C++ host-side mirror of the reference's per-token operator
+// interface over the C ABI of libt2h.so (t2h.h).
+//
+// The reference's host language is Mojo; this header keeps its operator
+// names, argument meaning, value semantics (inputs borrowed, a fresh output
+// tensor returned) and error texts (the reference's `raise Error("...")` is a
+// thrown t2h::Error with the same message), on device tensors whose every
+// op is a libt2h kernel:
+//   nn::LayerNorm32            modules/nn.mojo:297-375
+//   nn::modulate               modules/nn.mojo:660-689
+//   nn::activation             modules/nn.mojo:588-647
+//   nn::MultiHeadRMSNorm       sparse/attention/modules.mojo:37-102
+//   nn::RotaryPositionEmbedder, nn::apply_rotary_embedding
+//                              modules/rope.mojo:17-88
+//   nn::gate (_gate)           modules/transformer/modulated.mojo:22-33
+//   nn::TimestepEmbedder       models/sparse_structure_flow.mojo:40-80
+//   sparse::VarLenTensor, sparse::SparseTensor
+//                              sparse/basic.mojo:89-155, 296-339, 433-439
+//   sparse::mod_shift_scale    sparse/transformer/modulated.mojo:60-65
+//   sparse::Modulation         sparse/transformer/modulated.mojo:24-57
+//   sparse::SparseRotaryPositionEmbedder
+//                              sparse/attention/rope.mojo:20-134
+//
+// Calls run on the default HIP stream and are ordered with each other; a
+// host read (Tensor::to_host, the SparseTensor layout check) synchronises.
+// Output tensors are allocated per call (hipMalloc), as the reference
+// allocates a fresh Tensor per op; the device entry points of t2h.h are the
+// allocation-free hot path. Link with -lt2h (and the HIP runtime).
+#ifndef T2H_HPP
+#define T2H_HPP
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "t2h.h"
+
+namespace t2h {
+
+// The reference's Error: thrown with its message text.
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+inline void check(int32_t rc) {
+    if (rc != T2H_OK) throw Error(t2h_last_error());
+}
+
+inline void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+enum DType : int32_t { F32 = T2H_F32, F16 = T2H_F16, BF16 = T2H_BF16 };
+
+inline size_t dtype_size(DType d) { return d == F32 ? 4 : 2; }
+
+namespace detail {
+
+// f32 <-> f16 / bf16 storage, round to nearest even (host side).
+inline uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu)) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+inline float bf16_to_f32(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+inline uint16_t f32_to_f16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t)(sign | (a > 0x7F800000u ? 0x7E00u : 0x7C00u));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);   // >= 65520 rounds to inf
+    if (a < 0x38800000u) {                                      // below 2^-14: subnormal
+        float v;
+        std::memcpy(&v, &a, 4);
+        return (uint16_t)(sign | (uint32_t)std::nearbyint(v * 16777216.0f));   // units of 2^-24, ties to even
+    }
+    uint32_t h = ((((a >> 23) - 112u) << 10) | ((a & 0x7FFFFFu) >> 13));
+    const uint32_t rem = a & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+inline float f16_to_f32(uint16_t b) {
+    const uint32_t sign = (uint32_t)(b & 0x8000u) << 16, e = (b >> 10) & 0x1Fu, m = b & 0x3FFu;
+    uint32_t u;
+    if (e == 0) {
+        const float v = (float)m * (1.0f / 16777216.0f);
+        std::memcpy(&u, &v, 4);
+        u |= sign;
+    } else if (e == 31) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+inline std::shared_ptr<void> device_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (bytes > 0) check_hip(hipMalloc(&p, bytes), "hipMalloc");
+    return std::shared_ptr<void>(p, [](void* q) {
+        if (q != nullptr) (void)hipFree(q);
+    });
+}
+
+inline int64_t product(const std::vector<int64_t>& s) {
+    int64_t n = 1;
+    for (int64_t d : s) n *= d;
+    return n;
+}
+
+}  // namespace detail
+
+// Row-major device tensor with the reference Tensor's shape helpers
+// (sparse/tensor.mojo:122-135): rows() = shape[0], row_size() = the
+// product of the other dims. Copies share storage; ops return new tensors.
+class Tensor {
+public:
+    Tensor() = default;
+
+    static Tensor empty(std::vector<int64_t> shape, DType dt = F32) {
+        Tensor t;
+        t.shape_ = std::move(shape);
+        t.dtype_ = dt;
+        t.buf_ = detail::device_alloc((size_t)detail::product(t.shape_) * dtype_size(dt));
+        return t;
+    }
+
+    static Tensor zeros(std::vector<int64_t> shape, DType dt = F32) {
+        Tensor t = empty(std::move(shape), dt);
+        if (t.numel() > 0) check_hip(hipMemset(t.data(), 0, t.bytes()), "hipMemset");
+        return t;
+    }
+
+    // f32 host values stored in `dt` (rounded to nearest even for f16/bf16).
+    static Tensor from_host(const float* src, std::vector<int64_t> shape, DType dt = F32) {
+        Tensor t = empty(std::move(shape), dt);
+        const int64_t n = t.numel();
+        if (n == 0) return t;
+        if (dt == F32) {
+            check_hip(hipMemcpy(t.data(), src, t.bytes(), hipMemcpyHostToDevice), "hipMemcpy");
+        } else {
+            std::vector<uint16_t> h((size_t)n);
+            for (int64_t i = 0; i < n; ++i)
+                h[(size_t)i] = dt == F16 ? detail::f32_to_f16(src[i]) : detail::f32_to_bf16(src[i]);
+            check_hip(hipMemcpy(t.data(), h.data(), t.bytes(), hipMemcpyHostToDevice), "hipMemcpy");
+        }
+        return t;
+    }
+
+    // Tensor.from_values (sparse/tensor.mojo): shape + row-major values.
+    static Tensor from_values(std::vector<int64_t> shape, const std::vector<float>& values, DType dt = F32) {
+        if ((int64_t)values.size() != detail::product(shape)) throw Error("Tensor.from_values: size mismatch");
+        return from_host(values.data(), std::move(shape), dt);
+    }
+
+    // The values as f32 (synchronises).
+    std::vector<float> to_host() const {
+        std::vector<float> out((size_t)numel());
+        if (out.empty()) return out;
+        if (dtype_ == F32) {
+            check_hip(hipMemcpy(out.data(), data(), bytes(), hipMemcpyDeviceToHost), "hipMemcpy");
+        } else {
+            std::vector<uint16_t> h(out.size());
+            check_hip(hipMemcpy(h.data(), data(), bytes(), hipMemcpyDeviceToHost), "hipMemcpy");
+            for (size_t i = 0; i < h.size(); ++i)
+                out[i] = dtype_ == F16 ? detail::f16_to_f32(h[i]) : detail::bf16_to_f32(h[i]);
+        }
+        return out;
+    }
+
+    // Same storage, another shape of the same size.
+    Tensor reshape(std::vector<int64_t> shape) const {
+        if (detail::product(shape) != numel()) throw Error("Tensor.reshape: size mismatch");
+        Tensor t = *this;
+        t.shape_ = std::move(shape);
+        return t;
+    }
+
+    const std::vector<int64_t>& shape() const { return shape_; }
+    int64_t dim(int i) const { return shape_[(size_t)(i < 0 ? (int)shape_.size() + i : i)]; }
+    int ndim() const { return (int)shape_.size(); }
+    int64_t numel() const { return detail::product(shape_); }
+    int64_t rows() const { return shape_.empty() ? 1 : shape_[0]; }
+    int64_t row_size() const { return rows() == 0 ? 0 : numel() / rows(); }
+    size_t bytes() const { return (size_t)numel() * dtype_size(dtype_); }
+    DType dtype() const { return dtype_; }
+    void* data() const { return buf_.get(); }
+
+private:
+    std::shared_ptr<void> buf_;
+    std::vector<int64_t> shape_;
+    DType dtype_ = F32;
+};
+
+// int32 device matrix [rows, cols]: the reference's IntMatrix (sparse/tensor.mojo:59-70),
+// used for SparseTensor coords (b, x, y, z).
+class IntMatrix {
+public:
+    IntMatrix() = default;
+    static IntMatrix from_host(const int32_t* src, int64_t rows, int64_t cols) {
+        IntMatrix m;
+        m.rows_ = rows;
+        m.cols_ = cols;
+        m.buf_ = detail::device_alloc((size_t)(rows * cols) * 4);
+        if (rows * cols > 0)
+            check_hip(hipMemcpy(m.data(), src, (size_t)(rows * cols) * 4, hipMemcpyHostToDevice), "hipMemcpy");
+        return m;
+    }
+    std::vector<int32_t> to_host() const {
+        std::vector<int32_t> out((size_t)(rows_ * cols_));
+        if (!out.empty())
+            check_hip(hipMemcpy(out.data(), data(), out.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy");
+        return out;
+    }
+    int64_t rows() const { return rows_; }
+    int64_t cols() const { return cols_; }
+    int32_t* data() const { return static_cast<int32_t*>(buf_.get()); }
+
+private:
+    std::shared_ptr<void> buf_;
+    int64_t rows_ = 0, cols_ = 0;
+};
+
+namespace detail {
+
+inline std::vector<float> host_floats(const Tensor& t) {
+    if (t.dtype() != F32) throw Error("expected a float32 tensor");
+    return t.to_host();
+}
+
+inline const float* f32_ptr(const Tensor& t, const char* what) {
+    if (t.dtype() != F32) throw Error(std::string(what) + ": parameters must be float32");
+    return static_cast<const float*>(t.data());
+}
+
+}  // namespace detail
+
+// ---- modules/nn.mojo ---------------------------------------------------------
+namespace nn {
+
+constexpr int ACT_RELU = T2H_ACT_RELU, ACT_SILU = T2H_ACT_SILU, ACT_GELU = T2H_ACT_GELU,
+              ACT_GELU_TANH = T2H_ACT_GELU_TANH;   // modules/nn.mojo:582-585
+
+// nn.LayerNorm over the last dim (modules/nn.mojo:297-369): eps 1e-5 and
+// affine by default, weight ones and bias zeros.
+struct LayerNorm32 {
+    int64_t num_channels;
+    float eps;
+    bool affine;
+    Tensor weight, bias;
+
+    explicit LayerNorm32(int64_t channels, double eps_ = 1e-5, bool affine_ = true)
+        : num_channels(channels), eps((float)eps_), affine(affine_) {
+        std::vector<float> ones((size_t)channels, 1.0f);
+        weight = Tensor::from_host(ones.data(), {channels});
+        bias = Tensor::zeros({channels});
+    }
+
+    Tensor forward(const Tensor& x) const {
+        if (x.ndim() == 0 || x.dim(-1) != num_channels) throw Error("LayerNorm32: last dim mismatch");
+        const int64_t rows = x.numel() / num_channels;
+        Tensor out = Tensor::empty(x.shape(), x.dtype());
+        check(t2h_ln_modulate(x.data(), out.data(), rows, (int32_t)num_channels, x.dtype(), eps,
+                              affine ? T2H_LN_AFFINE : T2H_LN_PLAIN, affine ? (const float*)weight.data() : nullptr,
+                              affine ? (const float*)bias.data() : nullptr, 0, nullptr, 1, 0, nullptr));
+        return out;
+    }
+};
+
+// x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1): x [N, L, C], shift and
+// scale [N, C] (modules/nn.mojo:660-689). Bit-exact.
+inline Tensor modulate(const Tensor& x, const Tensor& shift, const Tensor& scale) {
+    if (x.ndim() != 3) throw Error("modulate: expected x [N, L, C]");
+    const int64_t n = x.dim(0), l = x.dim(1), c = x.dim(2);
+    if (shift.numel() != n * c || scale.numel() != n * c) throw Error("modulate: shift/scale shape mismatch");
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    check(t2h_modulate(x.data(), out.data(), n * l, (int32_t)c, x.dtype(), detail::f32_ptr(shift, "modulate"),
+                       detail::f32_ptr(scale, "modulate"), 0, nullptr, (int32_t)n, l, nullptr));
+    return out;
+}
+
+// Elementwise activation (modules/nn.mojo:588-647).
+inline Tensor activation(const Tensor& x, int kind) {
+    if (kind < ACT_RELU || kind > ACT_GELU_TANH) throw Error("unknown activation");
+    const int64_t c = x.ndim() ? x.dim(-1) : 1;
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    check(t2h_activation(x.data(), out.data(), nullptr, c ? x.numel() / c : 0, (int32_t)c, x.dtype(), kind,
+                         nullptr));
+    return out;
+}
+
+// F.normalize(x, dim=-1) * gamma * sqrt(dim) over x [..., H, D]
+// (sparse/attention/modules.mojo:37-102); gamma [H, D] starts at ones.
+struct MultiHeadRMSNorm {
+    int64_t dim, heads;
+    Tensor gamma;
+
+    MultiHeadRMSNorm(int64_t dim_, int64_t heads_) : dim(dim_), heads(heads_) {
+        std::vector<float> ones((size_t)(dim_ * heads_), 1.0f);
+        gamma = Tensor::from_host(ones.data(), {heads_, dim_});
+    }
+
+    Tensor forward(const Tensor& x) const {
+        if (x.ndim() < 2 || x.dim(-1) != dim || x.dim(-2) != heads)
+            throw Error("MultiHeadRMSNorm: gamma shape mismatch");
+        const int64_t rows = x.numel() / (dim * heads);
+        Tensor out = Tensor::empty(x.shape(), x.dtype());
+        check(t2h_qk_rmsnorm_rope(x.data(), nullptr, out.data(), nullptr, rows, 0, 0, (int32_t)heads, (int32_t)dim,
+                                  x.dtype(), nullptr, nullptr, detail::f32_ptr(gamma, "MultiHeadRMSNorm"), nullptr,
+                                  0, nullptr, 0, 3, nullptr, 0, nullptr, 0, 0, nullptr));
+        return out;
+    }
+};
+
+// freqs = freq_lo / freq_hi ** (arange(freq_dim) / freq_dim), f32
+// (modules/rope.mojo:33-37).
+inline std::vector<float> rope_freqs(int64_t head_dim, int64_t dim = 3, double freq_lo = 1.0,
+                                     double freq_hi = 10000.0) {
+    std::vector<float> f((size_t)(head_dim / 2 > 0 ? head_dim / 2 : 1));
+    const int32_t fd = t2h_rope_freqs((int32_t)head_dim, (int32_t)dim, freq_lo, freq_hi, f.data(), (int32_t)f.size());
+    if (fd < 0) check(fd);
+    f.resize((size_t)fd);
+    return f;
+}
+
+// Dense-path RoPE (modules/rope.mojo:17-61): forward(positions f32 [L, dim])
+// -> phases [L, head_dim/2, 2] (cos, sin); axis-major slots, unit pad slots.
+struct RotaryPositionEmbedder {
+    int64_t head_dim, dim, freq_dim;
+    std::vector<float> freqs;
+
+    explicit RotaryPositionEmbedder(int64_t head_dim_, int64_t dim_ = 3, double freq_lo = 1.0,
+                                    double freq_hi = 10000.0)
+        : head_dim(head_dim_), dim(dim_) {
+        if (head_dim_ % 2 != 0) throw Error("RotaryPositionEmbedder: head_dim must be even");
+        freq_dim = head_dim_ / 2 / dim_;
+        freqs = rope_freqs(head_dim_, dim_, freq_lo, freq_hi);
+    }
+
+    Tensor forward(const Tensor& positions) const {
+        if (positions.ndim() != 2 || positions.dim(1) != dim)
+            throw Error("RotaryPositionEmbedder: last dim of positions must be dim");
+        const int64_t l = positions.dim(0);
+        Tensor out = Tensor::empty({l, head_dim / 2, 2});
+        check(t2h_rope_phases(static_cast<float*>(out.data()), l, (int32_t)head_dim, freqs.data(),
+                              (int32_t)freqs.size(), (int32_t)dim, detail::f32_ptr(positions, "positions"), nullptr,
+                              0, 0, nullptr));
+        return out;
+    }
+};
+
+// x [N, L, H, D] (adjacent re/im pairs), phases [L, D/2, 2] broadcast over N
+// and H (modules/rope.mojo:64-88).
+inline Tensor apply_rotary_embedding(const Tensor& x, const Tensor& phases) {
+    if (x.ndim() != 4) throw Error("apply_rotary_embedding: expected [N, L, H, D]");
+    const int64_t n = x.dim(0), l = x.dim(1), h = x.dim(2), d = x.dim(3);
+    if (phases.ndim() != 3 || phases.dim(0) != l || phases.dim(1) != d / 2)
+        throw Error("apply_rotary_embedding: phases shape mismatch");
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    // no RMS and no frequency table: the phases are the position source
+    check(t2h_qk_rmsnorm_rope(x.data(), nullptr, out.data(), nullptr, n * l, 0, 0, (int32_t)h, (int32_t)d, x.dtype(),
+                              nullptr, nullptr, nullptr, nullptr, 1, nullptr, 0, 3,
+                              detail::f32_ptr(phases, "phases"), l, nullptr, 0, 0, nullptr));
+    return out;
+}
+
+// x [N, L, C] * g [N, C] broadcast over L (modules/transformer/modulated.mojo:22-33).
+inline Tensor gate(const Tensor& x, const Tensor& g) {
+    if (x.ndim() != 3) throw Error("_gate: expected x [N, L, C]");
+    const int64_t n = x.dim(0), l = x.dim(1), c = x.dim(2);
+    if (g.numel() != n * c) throw Error("_gate: gate shape mismatch");
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    check(t2h_gate_residual(nullptr, x.data(), out.data(), nullptr, detail::f32_ptr(g, "_gate"), 0, n * l,
+                            (int32_t)c, x.dtype(), nullptr, (int32_t)n, l, nullptr));
+    return out;
+}
+
+// Sinusoidal timestep embedding (models/sparse_structure_flow.mojo:40-80);
+// the MLP that follows it is a GEMM outside this path.
+struct TimestepEmbedder {
+    int64_t frequency_embedding_size;
+    double max_period;
+
+    explicit TimestepEmbedder(int64_t size = 256, double max_period_ = 10000.0)
+        : frequency_embedding_size(size), max_period(max_period_) {}
+
+    // t [N] f32 -> [N, frequency_embedding_size] f32
+    Tensor timestep_embedding(const Tensor& t) const {
+        const int64_t n = t.numel();
+        Tensor out = Tensor::empty({n, frequency_embedding_size});
+        check(t2h_timestep_embedding(detail::f32_ptr(t, "timestep_embedding"), out.data(), n,
+                                     (int32_t)frequency_embedding_size, T2H_F32, max_period, nullptr));
+        return out;
+    }
+};
+
+}  // namespace nn
+
+// ---- sparse/basic.mojo, sparse/transformer, sparse/attention ---------------------
+namespace sparse {
+
+constexpr int OP_ADD = T2H_OP_ADD, OP_SUB = T2H_OP_SUB, OP_MUL = T2H_OP_MUL,
+              OP_DIV = T2H_OP_DIV;   // sparse/tensor.mojo:4-7
+
+namespace detail {
+
+inline std::shared_ptr<void> device_offsets(const std::vector<int64_t>& offsets) {
+    auto p = t2h::detail::device_alloc(offsets.size() * 8);
+    check_hip(hipMemcpy(p.get(), offsets.data(), offsets.size() * 8, hipMemcpyHostToDevice), "hipMemcpy");
+    return p;
+}
+
+// feats [T, *] OP other[b(r)] with other [B, row] or [B, 1]
+inline Tensor binop_rows(const Tensor& feats, const Tensor& other, int op, const int64_t* dev_offsets,
+                         int64_t nbatch) {
+    const int64_t rows = feats.rows(), c = feats.row_size();
+    const int64_t oc = other.rows() ? other.numel() / other.rows() : 0;
+    if (other.dtype() != F32) throw Error("elemwise_batch: other must be float32");
+    Tensor out = Tensor::empty(feats.shape(), feats.dtype());
+    check(t2h_binop_rows(feats.data(), static_cast<const float*>(other.data()), out.data(), rows, (int32_t)c,
+                         (int32_t)oc, feats.dtype(), op, dev_offsets, (int32_t)nbatch, 0, nullptr));
+    return out;
+}
+
+}  // namespace detail
+
+// feats [T, *tail] with host offsets [B+1]: batch b owns rows
+// [offsets[b], offsets[b+1]) (sparse/basic.mojo:89-247).
+class VarLenTensor {
+public:
+    Tensor feats;
+    std::vector<int64_t> offsets;
+
+    VarLenTensor(Tensor f, std::vector<int64_t> offs) : feats(std::move(f)), offsets(std::move(offs)) {
+        bool ok = !offsets.empty() && offsets[0] == 0 && offsets.back() == feats.rows();
+        for (size_t i = 1; ok && i < offsets.size(); ++i) ok = offsets[i] >= offsets[i - 1];
+        if (!ok) throw Error("VarLenTensor: invalid offsets");
+        dev_ = detail::device_offsets(offsets);
+    }
+
+    int64_t batch_size() const { return (int64_t)offsets.size() - 1; }
+    int64_t seqlen(int64_t b) const { return offsets[(size_t)b + 1] - offsets[(size_t)b]; }
+    std::vector<int64_t> shape() const {
+        std::vector<int64_t> s{batch_size()};
+        s.insert(s.end(), feats.shape().begin() + 1, feats.shape().end());
+        return s;
+    }
+    // row -> batch (sparse/basic.mojo:149-155)
+    std::vector<int64_t> batch_broadcast_map() const {
+        std::vector<int64_t> m;
+        for (int64_t b = 0; b < batch_size(); ++b)
+            for (int64_t i = 0; i < seqlen(b); ++i) m.push_back(b);
+        return m;
+    }
+    VarLenTensor replace(Tensor f) const {
+        if (f.rows() != feats.rows()) throw Error("VarLenTensor.replace: row count mismatch");
+        VarLenTensor v = *this;
+        v.feats = std::move(f);
+        return v;
+    }
+    // feats[r] OP other[b(r)] (sparse/basic.mojo:204-207)
+    VarLenTensor elemwise_batch(const Tensor& other, int op) const {
+        if (other.rows() != batch_size()) throw Error("VarLenTensor.elemwise_batch: batch size mismatch");
+        return replace(detail::binop_rows(feats, other, op, static_cast<const int64_t*>(dev_.get()), batch_size()));
+    }
+    // feats OP value, or value OP feats when reverse (sparse/tensor.mojo:200-203)
+    VarLenTensor elemwise_scalar(float value, int op, bool reverse = false) const {
+        const Tensor v = Tensor::from_host(&value, {1, 1});
+        int o = op;
+        if (reverse && op == OP_SUB) o = T2H_OP_RSUB;
+        if (reverse && op == OP_DIV) o = T2H_OP_RDIV;
+        return replace(detail::binop_rows(feats, v, o, nullptr, 1));
+    }
+    VarLenTensor operator+(const VarLenTensor& o) const {
+        if (o.feats.numel() != feats.numel()) throw Error("Tensor binop: size mismatch");
+        Tensor out = Tensor::empty(feats.shape(), feats.dtype());
+        check(t2h_gate_residual(feats.data(), o.feats.data(), out.data(), nullptr, nullptr, 0, feats.rows(),
+                                (int32_t)feats.row_size(), feats.dtype(), nullptr, 1, 0, nullptr));
+        return replace(out);
+    }
+    VarLenTensor operator+(float v) const { return elemwise_scalar(v, OP_ADD); }
+    VarLenTensor operator-(float v) const { return elemwise_scalar(v, OP_SUB); }
+    VarLenTensor operator*(float v) const { return elemwise_scalar(v, OP_MUL); }
+    VarLenTensor operator/(float v) const { return elemwise_scalar(v, OP_DIV); }
+    VarLenTensor operator-() const { return elemwise_scalar(-1.0f, OP_MUL); }
+
+    const int64_t* device_offsets() const { return static_cast<const int64_t*>(dev_.get()); }
+
+private:
+    std::shared_ptr<void> dev_;
+};
+
+// feats [N, *tail] + int32 coords [N, 4] = (batch, x, y, z); the rows of a
+// batch contiguous and batches ordered. The offsets are computed on the
+// device from coords[:, 0] (sparse/basic.mojo:321-339) and checked on the
+// host, with the reference's two errors.
+class SparseTensor {
+public:
+    Tensor feats;
+    IntMatrix coords;
+
+    SparseTensor(Tensor f, IntMatrix c, int64_t batch_size = -1) : feats(std::move(f)), coords(std::move(c)) {
+        if (feats.rows() != coords.rows()) throw Error("SparseTensor: feats/coords row mismatch");
+        int64_t b = batch_size;
+        if (b < 0) {   // IntMatrix.col_max(0) + 1
+            if (coords.rows() == 0) throw Error("IntMatrix.col_max: empty matrix");
+            const std::vector<int32_t> h = coords.to_host();
+            int32_t mx = h[0];
+            for (int64_t r = 0; r < coords.rows(); ++r) mx = h[(size_t)(r * coords.cols())] > mx ? h[(size_t)(r * coords.cols())] : mx;
+            b = (int64_t)mx + 1;
+        }
+        batch_ = b;
+        dev_ = t2h::detail::device_alloc((size_t)(b + 2) * 8);   // offsets [B+1] + the first-bad flag
+        int64_t* off = static_cast<int64_t*>(dev_.get());
+        check(t2h_coords_to_offsets(coords.data(), coords.rows(), (int32_t)coords.cols(), (int32_t)b, off, off + b + 1,
+                                    nullptr));
+        std::vector<int64_t> h((size_t)(b + 2));
+        check_hip(hipMemcpy(h.data(), off, h.size() * 8, hipMemcpyDeviceToHost), "hipMemcpy");
+        const int64_t bad = h[(size_t)b + 1];
+        if (bad != INT64_MAX) {
+            if (bad & 1) throw Error("SparseTensor: batch index out of range");
+            throw Error("SparseTensor: batches must be ordered/contiguous");
+        }
+        offsets_.assign(h.begin(), h.begin() + b + 1);
+    }
+
+    int64_t batch_size() const { return batch_; }
+    int64_t seqlen(int64_t b) const { return offsets_[(size_t)b + 1] - offsets_[(size_t)b]; }
+    const std::vector<int64_t>& offsets() const { return offsets_; }
+    const int64_t* device_offsets() const { return static_cast<const int64_t*>(dev_.get()); }
+
+    SparseTensor replace(Tensor f) const {
+        if (f.rows() != feats.rows()) throw Error("VarLenTensor.replace: row count mismatch");
+        SparseTensor s = *this;
+        s.feats = std::move(f);
+        return s;
+    }
+    // the reference's x.vl
+    VarLenTensor vl() const { return VarLenTensor(feats, offsets_); }
+
+    // feats[r] OP other[b(r)] (sparse/basic.mojo:433-436)
+    SparseTensor elemwise_batch(const Tensor& other, int op) const {
+        if (other.rows() != batch_) throw Error("SparseTensor.elemwise_batch: batch size mismatch");
+        return replace(detail::binop_rows(feats, other, op, device_offsets(), batch_));
+    }
+    // elementwise feats add (sparse/basic.mojo:438-439)
+    SparseTensor operator+(const SparseTensor& o) const {
+        if (o.feats.numel() != feats.numel()) throw Error("Tensor binop: size mismatch");
+        Tensor out = Tensor::empty(feats.shape(), feats.dtype());
+        check(t2h_gate_residual(feats.data(), o.feats.data(), out.data(), nullptr, nullptr, 0, feats.rows(),
+                                (int32_t)feats.row_size(), feats.dtype(), nullptr, 1, 0, nullptr));
+        return replace(out);
+    }
+
+private:
+    int64_t batch_ = 0;
+    std::vector<int64_t> offsets_;
+    std::shared_ptr<void> dev_;
+};
+
+// h * (1 + scale) + shift with [B, C] batch broadcast (sparse/transformer/modulated.mojo:60-65).
+inline SparseTensor mod_shift_scale(const SparseTensor& h, const Tensor& shift, const Tensor& scale) {
+    if (shift.rows() != h.batch_size() || scale.rows() != h.batch_size())
+        throw Error("SparseTensor.elemwise_batch: batch size mismatch");
+    const int64_t c = h.feats.row_size();
+    Tensor out = Tensor::empty(h.feats.shape(), h.feats.dtype());
+    check(t2h_modulate(h.feats.data(), out.data(), h.feats.rows(), (int32_t)c, h.feats.dtype(),
+                       t2h::detail::f32_ptr(shift, "_mod_shift_scale"), t2h::detail::f32_ptr(scale, "_mod_shift_scale"),
+                       0, h.device_offsets(), (int32_t)h.batch_size(), 0, nullptr));
+    return h.replace(out);
+}
+
+// Modulation.chunks, share_mod branch (sparse/transformer/modulated.mojo:24-57):
+// m = mod [N, 6C] + modulation [6C] row-broadcast, returned as the six [N, C]
+// chunks shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp.
+struct Modulation {
+    Tensor modulation;   // [6C] f32
+
+    explicit Modulation(Tensor m) : modulation(std::move(m)) {}
+
+    std::vector<Tensor> chunks(const Tensor& mod, int64_t channels) const {
+        if (mod.ndim() != 2 || mod.dim(1) != 6 * channels || modulation.numel() != 6 * channels)
+            throw Error("Modulation: expected [N, 6C] modulation rows");
+        const int64_t n = mod.dim(0);
+        Tensor m = Tensor::empty({n, 6 * channels});
+        check(t2h_modulation_add(t2h::detail::f32_ptr(mod, "Modulation"), t2h::detail::f32_ptr(modulation, "Modulation"),
+                                 static_cast<float*>(m.data()), n, 6 * channels, nullptr));
+        std::vector<Tensor> out;
+        for (int64_t i = 0; i < 6; ++i) {   // slice_dim(1, i*C, (i+1)*C): a fresh [N, C] tensor
+            Tensor t = Tensor::empty({n, channels});
+            if (n > 0)
+                check_hip(hipMemcpy2D(t.data(), (size_t)channels * 4, static_cast<float*>(m.data()) + i * channels,
+                                      (size_t)(6 * channels) * 4, (size_t)channels * 4, (size_t)n,
+                                      hipMemcpyDeviceToDevice),
+                          "hipMemcpy2D");
+            out.push_back(t);
+        }
+        return out;
+    }
+};
+
+// RoPE from int voxel coords (sparse/attention/rope.mojo:20-134): embed
+// rotates q and k (feats [N, H, head_dim]) in one kernel, the phases coming
+// from each row's coords.
+struct SparseRotaryPositionEmbedder {
+    int64_t head_dim, dim, freq_dim;
+    std::vector<float> freqs;
+
+    explicit SparseRotaryPositionEmbedder(int64_t head_dim_, int64_t dim_ = 3, double freq_lo = 1.0,
+                                          double freq_hi = 10000.0)
+        : head_dim(head_dim_), dim(dim_) {
+        if (head_dim_ % 2 != 0) throw Error("SparseRotaryPositionEmbedder: head_dim must be even");
+        freq_dim = head_dim_ / 2 / dim_;
+        freqs = nn::rope_freqs(head_dim_, dim_, freq_lo, freq_hi);
+    }
+
+    // _compute_phases: [N, head_dim/2, 2] (sparse/attention/rope.mojo:48-66)
+    Tensor compute_phases(const SparseTensor& x) const {
+        if (x.coords.cols() != dim + 1) throw Error("rope: coords must have dim+1 columns");
+        Tensor out = Tensor::empty({x.coords.rows(), head_dim / 2, 2});
+        check(t2h_rope_phases(static_cast<float*>(out.data()), x.coords.rows(), (int32_t)head_dim, freqs.data(),
+                              (int32_t)freqs.size(), (int32_t)dim, nullptr, x.coords.data(), (int32_t)x.coords.cols(),
+                              0, nullptr));
+        return out;
+    }
+
+    std::pair<SparseTensor, SparseTensor> embed(const SparseTensor& q, const SparseTensor& k) const {
+        if (q.coords.cols() != dim + 1) throw Error("rope: coords must have dim+1 columns");
+        if (q.feats.dim(-1) != head_dim || k.feats.dim(-1) != head_dim) throw Error("rope: feats last dim != head_dim");
+        if (q.feats.numel() != k.feats.numel() || q.feats.dtype() != k.feats.dtype())
+            throw Error("rope: q/k shape mismatch");
+        const int64_t rows = q.feats.rows();
+        const int64_t heads = q.feats.row_size() / head_dim;
+        Tensor qo = Tensor::empty(q.feats.shape(), q.feats.dtype());
+        Tensor ko = Tensor::empty(k.feats.shape(), k.feats.dtype());
+        check(t2h_qk_rmsnorm_rope(q.feats.data(), k.feats.data(), qo.data(), ko.data(), rows, 0, 0, (int32_t)heads,
+                                  (int32_t)head_dim, q.feats.dtype(), nullptr, nullptr, nullptr, nullptr, 1,
+                                  freqs.data(), (int32_t)freqs.size(), (int32_t)dim, nullptr, 0, q.coords.data(),
+                                  (int32_t)q.coords.cols(), 0, nullptr));
+        return {q.replace(qo), k.replace(ko)};
+    }
+};
+
+}  // namespace sparse
+}  // namespace t2h
+
+#endif  // T2H_HPP

@@ -1,0 +1,433 @@
+// Tests of the C++ operator interface (include/t2h.hpp) on the GPU.
+//
+// The hand-computed cases are those of the reference's
+// tests/parity/test_sparse_basic.mojo (make_varlen 21-25, make_sparse 28-43,
+// layout 47-59, elemwise 73-91, sparse layout 149-158, contiguity 161-171);
+// the numeric ops are checked against the C oracle (liboracle.so, the CPU
+// restatement of the reference) on seeded inputs, bit for bit where the op
+// has no reduction or transcendental, else with
+//   err = |got - want| / max(|want|, 1) <= 1e-5 (f32 storage), 2e-3 (f16).
+//
+// Usage: test_t2h_cpp [name-substring]   (exit status 0 = all passed)
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "t2h.hpp"
+
+extern "C" {
+#include "oracle.h"
+}
+
+using t2h::Error;
+using t2h::IntMatrix;
+using t2h::Tensor;
+namespace nn = t2h::nn;
+namespace sp = t2h::sparse;
+
+namespace {
+
+struct Failure {
+    std::string what;
+};
+
+#define EXPECT(cond)                                                                  \
+    do {                                                                              \
+        if (!(cond)) throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " #cond}; \
+    } while (0)
+
+std::vector<float> randn(uint64_t seed, int64_t n, double std = 1.0) {
+    orc_rng r;
+    orc_rng_init(&r, seed);
+    std::vector<float> v((size_t)n);
+    orc_randn(&r, v.data(), n, 0.0, std);
+    return v;
+}
+
+std::vector<float> round_f16(const std::vector<float>& x) {
+    std::vector<float> o(x.size());
+    orc_round_f16(x.data(), o.data(), (int64_t)x.size());
+    return o;
+}
+
+double max_err(const std::vector<float>& got, const std::vector<float>& want) {
+    if (got.size() != want.size()) throw Failure{"size mismatch"};
+    double m = 0.0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        if (!std::isfinite(got[i])) return INFINITY;
+        const double e = std::fabs((double)got[i] - want[i]) / std::fmax(std::fabs((double)want[i]), 1.0);
+        m = e > m ? e : m;
+    }
+    return m;
+}
+
+void expect_close(const std::vector<float>& got, const std::vector<float>& want, double tol, const char* what) {
+    const double e = max_err(got, want);
+    std::printf("    %s: max err %.3e (tol %g)\n", what, e, tol);
+    if (!(e <= tol)) throw Failure{std::string(what) + ": max err " + std::to_string(e)};
+}
+
+void expect_bits(const std::vector<float>& got, const std::vector<float>& want, const char* what) {
+    if (got.size() != want.size() || std::memcmp(got.data(), want.data(), got.size() * 4) != 0)
+        throw Failure{std::string(what) + ": not bit-exact"};
+    std::printf("    %s: bit-exact (%zu values)\n", what, got.size());
+}
+
+template <class F>
+void expect_error(F&& f, const char* text) {
+    try {
+        f();
+    } catch (const Error& e) {
+        if (std::strstr(e.what(), text) == nullptr)
+            throw Failure{std::string("wrong error: '") + e.what() + "', expected '" + text + "'"};
+        return;
+    }
+    throw Failure{std::string("no error raised, expected '") + text + "'"};
+}
+
+// ---- tests/parity/test_sparse_basic.mojo ------------------------------------------
+sp::VarLenTensor make_varlen() {   // 21-25
+    return sp::VarLenTensor(Tensor::from_values({5, 2}, {1, 2, 3, 4, 5, 6, 7, 8, 9, 10}), {0, 2, 5});
+}
+
+sp::SparseTensor make_sparse() {   // 28-43
+    const int32_t c[5][4] = {{0, 0, 0, 0}, {0, 1, 0, 1}, {1, 0, 1, 0}, {1, 1, 1, 1}, {1, 1, 0, 0}};
+    return sp::SparseTensor(Tensor::from_values({5, 2}, {1, 2, 3, 4, 5, 6, 7, 8, 9, 10}),
+                            IntMatrix::from_host(&c[0][0], 5, 4));
+}
+
+void test_varlen_shape_and_layout() {   // 47-59
+    const auto x = make_varlen();
+    EXPECT(x.batch_size() == 2);
+    EXPECT(x.shape()[0] == 2 && x.shape()[1] == 2);
+    EXPECT(x.seqlen(0) == 2 && x.seqlen(1) == 3);
+    const auto bm = x.batch_broadcast_map();
+    EXPECT(bm[0] == 0 && bm[1] == 0 && bm[2] == 1 && bm[4] == 1);
+    expect_error([] { sp::VarLenTensor(Tensor::zeros({5, 2}), {0, 3, 2, 5}); }, "VarLenTensor: invalid offsets");
+}
+
+void test_varlen_elemwise() {   // 73-91, plus the reverse scalar forms
+    const auto x = make_varlen();
+    const auto y = ((x + 1.0f) * 2.0f).feats.to_host();
+    EXPECT(y[0] == 4.0f && y[9] == 22.0f);
+    EXPECT((x + x).feats.to_host()[3] == 8.0f);
+    EXPECT((-x).feats.to_host()[0] == -1.0f);
+    const auto w = x.elemwise_batch(Tensor::from_values({2, 1}, {10, 100}), sp::OP_ADD).feats.to_host();
+    EXPECT(w[0] == 11.0f && w[4] == 105.0f);
+    const auto w2 = x.elemwise_batch(Tensor::from_values({2, 2}, {10, 20, 100, 200}), sp::OP_ADD).feats.to_host();
+    EXPECT(w2[1] == 22.0f && w2[9] == 210.0f);
+    const auto f = x.feats.to_host();
+    for (int op = sp::OP_ADD; op <= sp::OP_DIV; ++op)
+        for (int rev = 0; rev < 2; ++rev) {
+            std::vector<float> want(f.size());
+            orc_binop_scalar(f.data(), 3.0f, want.data(), (int64_t)f.size(), op, rev);
+            expect_bits(x.elemwise_scalar(3.0f, op, rev != 0).feats.to_host(), want, "elemwise_scalar");
+        }
+    expect_error([&] { x.elemwise_batch(Tensor::zeros({3, 1}), sp::OP_ADD); }, "batch size mismatch");
+}
+
+void test_sparse_layout_from_coords() {   // 149-158
+    const auto x = make_sparse();
+    EXPECT(x.batch_size() == 2);
+    EXPECT(x.seqlen(0) == 2 && x.seqlen(1) == 3);
+    EXPECT((x.offsets() == std::vector<int64_t>{0, 2, 5}));
+    const auto v = x.vl();
+    EXPECT(v.batch_size() == 2 && v.seqlen(1) == 3);
+}
+
+void test_sparse_contiguity_enforced() {   // 161-171, and the out-of-range branch
+    expect_error(
+        [] {
+            const int32_t c[2][4] = {{1, 0, 0, 0}, {0, 0, 0, 0}};   // batch 1 before batch 0
+            sp::SparseTensor(Tensor::zeros({2, 1}), IntMatrix::from_host(&c[0][0], 2, 4));
+        },
+        "ordered/contiguous");
+    expect_error(
+        [] {
+            const int32_t c[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {5, 0, 0, 0}};
+            sp::SparseTensor(Tensor::zeros({3, 1}), IntMatrix::from_host(&c[0][0], 3, 4), 2);
+        },
+        "out of range");
+    expect_error([] { sp::SparseTensor(Tensor::zeros({2, 1}), IntMatrix::from_host(nullptr, 0, 4)); },
+                 "feats/coords row mismatch");
+}
+
+void test_sparse_elemwise_batch() {
+    const auto x = make_sparse();
+    const Tensor b = Tensor::from_values({2, 2}, {10, 20, 100, 200});
+    const auto y = x.elemwise_batch(b, sp::OP_ADD).feats.to_host();
+    EXPECT(y[0] == 11.0f && y[9] == 210.0f);
+    EXPECT(x.elemwise_batch(b, sp::OP_MUL).feats.to_host()[1] == 40.0f);
+    const auto s = x.elemwise_batch(Tensor::from_values({2, 1}, {10, 100}), sp::OP_ADD).feats.to_host();
+    EXPECT(s[0] == 11.0f && s[4] == 105.0f);
+    EXPECT((x + x).feats.to_host()[9] == 20.0f);
+}
+
+// ---- numeric parity against the oracle -------------------------------------------
+void test_layernorm32() {
+    const int64_t rows = 67, c = 1536;
+    const auto x = randn(1, rows * c, 2.0);
+    const auto w = randn(2, c, 0.5), b = randn(3, c, 0.5);
+    for (t2h::DType dt : {t2h::F32, t2h::F16}) {
+        const auto xin = dt == t2h::F32 ? x : round_f16(x);
+        nn::LayerNorm32 ln(c);   // eps 1e-5, affine, weight ones / bias zeros
+        std::vector<float> want((size_t)(rows * c));
+        const std::vector<float> ones((size_t)c, 1.0f), zeros((size_t)c, 0.0f);
+        orc_layernorm(xin.data(), want.data(), rows, c, 1e-5, 1, ones.data(), zeros.data());
+        const Tensor xd = Tensor::from_host(x.data(), {rows, c}, dt);
+        const double tol = dt == t2h::F32 ? 1e-5 : 2e-3;
+        expect_close(ln.forward(xd).to_host(), want, tol, "LayerNorm32 default params");
+        ln.weight = Tensor::from_host(w.data(), {c});
+        ln.bias = Tensor::from_host(b.data(), {c});
+        orc_layernorm(xin.data(), want.data(), rows, c, 1e-5, 1, w.data(), b.data());
+        expect_close(ln.forward(xd).to_host(), want, tol, "LayerNorm32 affine");
+        nn::LayerNorm32 plain(c, 1e-6, false);
+        orc_layernorm(xin.data(), want.data(), rows, c, 1e-6, 0, nullptr, nullptr);
+        expect_close(plain.forward(xd.reshape({1, rows, c})).to_host(), want, tol, "LayerNorm32 no affine");
+    }
+    expect_error([] { nn::LayerNorm32(8).forward(Tensor::zeros({2, 9})); }, "LayerNorm32: last dim mismatch");
+}
+
+void test_modulate_and_gate() {
+    const int64_t n = 3, l = 41, c = 1024;
+    const auto x = randn(4, n * l * c), sh = randn(5, n * c, 0.1), sc = randn(6, n * c, 0.1);
+    const Tensor xd = Tensor::from_host(x.data(), {n, l, c});
+    const Tensor shd = Tensor::from_host(sh.data(), {n, c}), scd = Tensor::from_host(sc.data(), {n, c});
+    std::vector<float> want((size_t)(n * l * c));
+    orc_modulate(x.data(), sh.data(), sc.data(), want.data(), n, l, c);
+    expect_bits(nn::modulate(xd, shd, scd).to_host(), want, "modulate");
+    orc_gate(x.data(), sc.data(), want.data(), n, l, c);
+    expect_bits(nn::gate(xd, scd).to_host(), want, "_gate");
+    expect_error([&] { nn::modulate(xd, Tensor::zeros({n, c - 1}), scd); }, "modulate: shift/scale shape mismatch");
+}
+
+void test_mod_shift_scale_sparse() {
+    // three batches, the middle one empty
+    const int64_t rows = 300, c = 1536;
+    std::vector<int32_t> coords((size_t)rows * 4, 0);
+    for (int64_t r = 0; r < rows; ++r) coords[(size_t)r * 4] = r < 120 ? 0 : 2;
+    const auto x = randn(7, rows * c), sh = randn(8, 3 * c, 0.1), sc = randn(9, 3 * c, 0.1);
+    const sp::SparseTensor h(Tensor::from_host(x.data(), {rows, c}), IntMatrix::from_host(coords.data(), rows, 4), 3);
+    EXPECT((h.offsets() == std::vector<int64_t>{0, 120, 120, 300}));
+    std::vector<int64_t> off(4);
+    EXPECT(orc_cal_offsets(coords.data(), rows, 4, 3, off.data()) == 0);
+    EXPECT(off == h.offsets());
+    std::vector<float> want((size_t)(rows * c));
+    orc_mod_shift_scale(x.data(), sh.data(), sc.data(), off.data(), 3, want.data(), rows, c);
+    const auto got = sp::mod_shift_scale(h, Tensor::from_host(sh.data(), {3, c}), Tensor::from_host(sc.data(), {3, c}));
+    expect_bits(got.feats.to_host(), want, "_mod_shift_scale");
+    expect_error([&] { sp::mod_shift_scale(h, Tensor::zeros({2, c}), Tensor::zeros({2, c})); }, "batch size mismatch");
+}
+
+void test_activation() {
+    const int64_t rows = 33, c = 1000;
+    const auto x = randn(10, rows * c, 3.0);
+    const Tensor xd = Tensor::from_host(x.data(), {rows, c});
+    for (int kind : {nn::ACT_RELU, nn::ACT_SILU, nn::ACT_GELU, nn::ACT_GELU_TANH}) {
+        std::vector<float> want(x.size());
+        EXPECT(orc_activation(x.data(), want.data(), rows * c, kind, 1) == 0);
+        expect_close(nn::activation(xd, kind).to_host(), want, 1e-5, "activation");
+    }
+    expect_error([&] { nn::activation(xd, 7); }, "unknown activation");
+}
+
+void test_multihead_rmsnorm_and_rope() {
+    // MultiHeadRMSNorm then apply_rotary_embedding(x [N, L, H, D], phases) with
+    // RotaryPositionEmbedder.forward(grid positions), the dense attention order
+    const int64_t n = 2, res = 4, l = res * res * res, h = 12, d = 128;
+    const auto q = randn(11, n * l * h * d), g = randn(12, h * d, 0.5);
+    nn::MultiHeadRMSNorm rms(d, h);
+    rms.gamma = Tensor::from_host(g.data(), {h, d});
+    std::vector<float> pos((size_t)(l * 3));
+    orc_grid_positions(res, pos.data());
+    nn::RotaryPositionEmbedder emb(d);
+    std::vector<float> freqs((size_t)(d / 2));
+    const int64_t fd = orc_rope_freqs(d, 3, 1.0, 10000.0, freqs.data());
+    EXPECT(fd == emb.freq_dim && (int64_t)emb.freqs.size() == fd);
+    EXPECT(std::memcmp(freqs.data(), emb.freqs.data(), (size_t)fd * 4) == 0);
+    std::vector<float> ph_want((size_t)(l * d));
+    EXPECT(orc_rope_phases_from_positions(pos.data(), l, 3, d, freqs.data(), fd, ph_want.data()) == 0);
+    const Tensor phases = emb.forward(Tensor::from_host(pos.data(), {l, 3}));
+    expect_close(phases.to_host(), ph_want, 1e-5, "RotaryPositionEmbedder.forward");
+
+    std::vector<float> normed(q.size()), want(q.size());
+    EXPECT(orc_multihead_rmsnorm(q.data(), g.data(), normed.data(), n * l, h, d, 1) == 0);
+    const Tensor qd = Tensor::from_host(q.data(), {n, l, h, d});
+    const Tensor got_rms = rms.forward(qd);
+    expect_close(got_rms.to_host(), normed, 1e-5, "MultiHeadRMSNorm");
+    EXPECT(orc_apply_rotary(normed.data(), ph_want.data(), want.data(), n, l, h, d) == 0);
+    expect_close(nn::apply_rotary_embedding(got_rms, phases).to_host(), want, 1e-5,
+                 "MultiHeadRMSNorm + apply_rotary_embedding");
+    expect_error([&] { nn::MultiHeadRMSNorm(64, h).forward(qd); }, "MultiHeadRMSNorm: gamma shape mismatch");
+    expect_error([] { nn::RotaryPositionEmbedder(63); }, "head_dim must be even");
+}
+
+void test_sparse_rope_embed() {
+    // SparseRotaryPositionEmbedder.embed(q, k) on voxel coords, f32 and f16
+    const int64_t rows = 515, h = 12, d = 128, res = 64;
+    std::vector<int32_t> coords((size_t)rows * 4);
+    orc_rng r;
+    orc_rng_init(&r, 13);
+    for (int64_t i = 0; i < rows; ++i) {
+        coords[(size_t)i * 4] = i < 200 ? 0 : 1;
+        for (int a = 1; a < 4; ++a) coords[(size_t)i * 4 + a] = (int32_t)(orc_rng_next_u64(&r) % res);
+    }
+    const auto q = randn(14, rows * h * d), k = randn(15, rows * h * d);
+    sp::SparseRotaryPositionEmbedder emb(d);
+    std::vector<float> ph((size_t)(rows * d));
+    EXPECT(orc_rope_phases_from_coords(coords.data(), rows, 4, 3, d, emb.freqs.data(), emb.freq_dim, ph.data()) == 0);
+    const IntMatrix cm = IntMatrix::from_host(coords.data(), rows, 4);
+    for (t2h::DType dt : {t2h::F32, t2h::F16}) {
+        const auto qi = dt == t2h::F32 ? q : round_f16(q), ki = dt == t2h::F32 ? k : round_f16(k);
+        const sp::SparseTensor sq(Tensor::from_host(q.data(), {rows, h, d}, dt), cm, 2);
+        const sp::SparseTensor sk(Tensor::from_host(k.data(), {rows, h, d}, dt), cm, 2);
+        if (dt == t2h::F32) expect_close(emb.compute_phases(sq).to_host(), ph, 1e-5, "_compute_phases");
+        std::vector<float> wq(q.size()), wk(k.size());
+        EXPECT(orc_rope_rotate(qi.data(), ph.data(), wq.data(), rows, h, d, 1) == 0);
+        EXPECT(orc_rope_rotate(ki.data(), ph.data(), wk.data(), rows, h, d, 1) == 0);
+        const auto qk = emb.embed(sq, sk);
+        const double tol = dt == t2h::F32 ? 1e-5 : 2e-3;
+        expect_close(qk.first.feats.to_host(), wq, tol, "embed q");
+        expect_close(qk.second.feats.to_host(), wk, tol, "embed k");
+    }
+}
+
+void test_timestep_embedder() {
+    orc_rng r;
+    orc_rng_init(&r, 501);
+    std::vector<float> t(64);
+    orc_uniform(&r, t.data(), 64, 0.0, 1.0);
+    for (float& v : t) v *= 1000.0f;   // the pipeline passes t * 1000
+    for (int64_t dim : {256, 255}) {
+        nn::TimestepEmbedder te(dim);
+        std::vector<float> want((size_t)(64 * dim));
+        orc_timestep_embedding(t.data(), 64, dim, 10000.0, want.data());
+        expect_close(te.timestep_embedding(Tensor::from_host(t.data(), {64})).to_host(), want, 1e-5,
+                     "timestep_embedding");
+    }
+}
+
+void test_modulation_chunks() {
+    const int64_t n = 2, c = 1536;
+    const auto mod = randn(16, n * 6 * c), par = randn(17, 6 * c, 0.02);
+    sp::Modulation m(Tensor::from_host(par.data(), {6 * c}));
+    const auto chunks = m.chunks(Tensor::from_host(mod.data(), {n, 6 * c}), c);
+    EXPECT(chunks.size() == 6);
+    std::vector<float> full((size_t)(n * 6 * c));
+    orc_modulation_add(mod.data(), par.data(), full.data(), n, 6 * c);
+    for (int64_t i = 0; i < 6; ++i) {
+        std::vector<float> want((size_t)(n * c));
+        for (int64_t b = 0; b < n; ++b)
+            std::memcpy(&want[(size_t)(b * c)], &full[(size_t)(b * 6 * c + i * c)], (size_t)c * 4);
+        expect_bits(chunks[(size_t)i].to_host(), want, "Modulation chunk");
+    }
+    expect_error([&] { m.chunks(Tensor::zeros({n, 5 * c}), c); }, "Modulation: expected [N, 6C] modulation rows");
+}
+
+// ---- host side of the header (no GPU) ------------------------------------------------
+bool same_value(float a, float b) {
+    if (std::isnan(a) || std::isnan(b)) return std::isnan(a) && std::isnan(b);
+    return std::memcmp(&a, &b, 4) == 0;
+}
+
+void test_host_f16_conversion() {
+    // every f16 pattern decodes as the oracle's, and encodes back to itself
+    for (uint32_t h = 0; h < 65536; ++h) {
+        const float f = t2h::detail::f16_to_f32((uint16_t)h);
+        EXPECT(same_value(f, orc_f16_to_f32((uint16_t)h)));
+        if (!std::isnan(f)) EXPECT(t2h::detail::f32_to_f16(f) == h);
+    }
+    // f32 -> f16 on random bit patterns and the rounding boundaries
+    orc_rng r;
+    orc_rng_init(&r, 99);
+    std::vector<float> xs = {0.0f, -0.0f, 65504.0f, 65519.99f, 65520.0f, 65536.0f, 1e-8f, 2.98e-8f, 2.9802322e-8f,
+                             5.9604645e-8f, 6.1035156e-5f, 6.097555e-5f, INFINITY, -INFINITY, NAN};
+    for (int i = 0; i < 1 << 20; ++i) {
+        const uint32_t u = (uint32_t)orc_rng_next_u64(&r);
+        float f;
+        std::memcpy(&f, &u, 4);
+        xs.push_back(f);
+        xs.push_back(std::ldexp((float)(u >> 8), -40 + (int)(u & 63)));   // the f16 range, finely
+    }
+    for (float f : xs) {
+        const uint16_t got = t2h::detail::f32_to_f16(f), want = orc_f32_to_f16(f);
+        if (std::isnan(f)) {
+            EXPECT((got & 0x7C00u) == 0x7C00u && (got & 0x3FFu) != 0);
+        } else if (got != want) {
+            throw Failure{"f32_to_f16 differs at " + std::to_string(f)};
+        }
+    }
+    std::vector<float> rb(xs.size());
+    orc_round_bf16(xs.data(), rb.data(), (int64_t)xs.size());
+    for (size_t i = 0; i < xs.size(); ++i)
+        EXPECT(same_value(t2h::detail::bf16_to_f32(t2h::detail::f32_to_bf16(xs[i])), rb[i]));
+    std::printf("    f16 / bf16 storage conversions equal the oracle's (%zu values)\n", xs.size());
+}
+
+void test_abi_errors_propagate() {
+    // a status from libt2h arrives as t2h::Error with the library's message
+    expect_error([] { nn::rope_freqs(7); }, "head_dim");
+    expect_error([] { nn::TimestepEmbedder(4096).timestep_embedding(Tensor::zeros({2})); }, "timestep");
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const std::vector<std::pair<const char*, std::function<void()>>> tests = {
+        {"varlen_shape_and_layout", test_varlen_shape_and_layout},
+        {"varlen_elemwise", test_varlen_elemwise},
+        {"sparse_layout_from_coords", test_sparse_layout_from_coords},
+        {"sparse_contiguity_enforced", test_sparse_contiguity_enforced},
+        {"sparse_elemwise_batch", test_sparse_elemwise_batch},
+        {"layernorm32", test_layernorm32},
+        {"modulate_and_gate", test_modulate_and_gate},
+        {"mod_shift_scale_sparse", test_mod_shift_scale_sparse},
+        {"activation", test_activation},
+        {"multihead_rmsnorm_and_rope", test_multihead_rmsnorm_and_rope},
+        {"sparse_rope_embed", test_sparse_rope_embed},
+        {"timestep_embedder", test_timestep_embedder},
+        {"modulation_chunks", test_modulation_chunks},
+        {"abi_errors_propagate", test_abi_errors_propagate},
+    };
+    if (argc > 1 && std::strcmp(argv[1], "--host") == 0) {   // the checks that need no GPU
+        try {
+            std::printf("test host_f16_conversion\n");
+            test_host_f16_conversion();
+            std::printf("ok host_f16_conversion\n");
+            return 0;
+        } catch (const Failure& f) {
+            std::printf("FAIL host_f16_conversion: %s\n", f.what.c_str());
+            return 1;
+        }
+    }
+    const char* filter = argc > 1 ? argv[1] : nullptr;
+    if (t2h_device_init(0) != T2H_OK) {
+        std::printf("t2h_device_init: %s\n", t2h_last_error());
+        return 2;
+    }
+    int failed = 0, ran = 0;
+    for (const auto& t : tests) {
+        if (filter != nullptr && std::strstr(t.first, filter) == nullptr) continue;
+        std::printf("test %s\n", t.first);
+        std::fflush(stdout);
+        ++ran;
+        try {
+            t.second();
+            std::printf("ok %s\n", t.first);
+        } catch (const Failure& f) {
+            ++failed;
+            std::printf("FAIL %s: %s\n", t.first, f.what.c_str());
+        } catch (const std::exception& e) {
+            ++failed;
+            std::printf("FAIL %s: unexpected exception: %s\n", t.first, e.what());
+        }
+        std::fflush(stdout);
+    }
+    std::printf("%d of %d passed\n", ran - failed, ran);
+    return failed == 0 && ran > 0 ? 0 : 1;
+}
