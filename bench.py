@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
     p.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1-4")
+    p.add_argument("--configs-only", action="store_true",
+                   help="time only BASELINE configs 1-4 and print their JSON (for profiler runs)")
     p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
     p.add_argument("--probe", action="store_true",
                    help="time the HBM streaming probes (lib/libhbm_probe.so) instead of the chain")
@@ -434,6 +436,17 @@ def other_configs(torch, dev, cpu=True):
             f"({nbytes/ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
         del fns
 
+    # The fixed cost of one launch under this protocol: a t2h kernel on one
+    # 64-element row, bracketed by the same two events.
+    tiny, tiny_o = rn((1, 64)), torch.empty(1, 64, device=dev)
+    tiny_fn = lambda: ops.activation(tiny, 0, out=tiny_o)
+    for _ in range(3):
+        tiny_fn()
+    fw, fc = time_op(torch, tiny_fn, 30), time_op(torch, tiny_fn, 30, flush)
+    res["launch_floor"] = {"warm_us": round(fw * 1e3, 2), "cold_us": round(fc * 1e3, 2),
+                           "what": "one t2h launch on a 64-element row, timed as the configs are"}
+    log(f"  launch floor (64-element kernel): warm {fw*1e3:.1f} us, cold {fc*1e3:.1f} us")
+
     C = 1536
     x = rn((4096, C)); sh = rn((C,), 0.1); sc = rn((C,), 0.1); out = torch.empty_like(x)
     hx, hsh, hsc = hst(x), hst(sh), hst(sc)
@@ -699,6 +712,10 @@ def main():
     ops.device_init(0)
     if args.probe:
         hbm_probes(torch, dev, args.steps)
+        return
+    if args.configs_only:
+        log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
+        print(json.dumps({"configs": other_configs(torch, dev, cpu=not args.no_cpu)}), flush=True)
         return
     dtype = torch.float16
     chain = Chain(dev, dtype)
