@@ -2,7 +2,7 @@
 // batch-broadcast binop, sinusoidal timestep embedding, coords -> batch
 // offsets, share_mod modulation add.
 //
-// Row-tiled layout: a block covers RPT consecutive rows and blockDim * V
+// Row-tiled layout: a block covers RPT consecutive rows and block_threads * V
 // columns (V = 16 B of storage per thread; one whole row when it fits). Per-column parameters (bias)
 // are loaded once per thread; per-batch parameter rows (gate, shift/scale,
 // `other`) are reloaded only when the tile's row crosses a batch boundary
@@ -57,7 +57,7 @@ struct Tile {
 };
 
 // Tile of this block, 1-D grid. When a row is a whole number of waves of
-// 16-byte vectors (cols / V = blockDim.x <= 1024), a block is exactly one row
+// 16-byte vectors (cols / V = block_threads <= 1024), a block is exactly one row
 // wide and covers kRpt full rows: every thread is busy and the block streams
 // one contiguous span. Otherwise blocks are kBlock * V columns wide and
 // consecutive blocks walk the column tiles of a row tile first, so blocks
@@ -74,7 +74,7 @@ __device__ __forceinline__ bool tile_of(const EltArgs& a, Tile& t) {
         rt = b / a.col_tiles;
         cb = b - rt * a.col_tiles;
     }
-    t.col0 = (cb * blockDim.x + threadIdx.x) * V;
+    t.col0 = (cb * a.block_threads + threadIdx.x) * V;
     t.r0 = rt * kRpt;
     if (t.r0 >= a.rows) return false;   // past the last row tile of a 2-D grid
     const int64_t left = a.rows - t.r0;
@@ -331,6 +331,7 @@ hipError_t tile_launch(K kernel, EltArgs a, hipStream_t s) {
     const int64_t ct = (a.cols + bw - 1) / bw;
     a.col_tiles = (int32_t)ct;
     a.fper = front_per(rt * ct);
+    a.block_threads = tile_block<V>(a);
     hipLaunchKernelGGL(kernel, grid_1d(front_grid(rt * ct)), dim3(tile_block<V>(a)), 0, s, a);
     return hipGetLastError();
 }

@@ -213,6 +213,8 @@ struct EltArgs {
     BatchArgs batch;
     int32_t col_tiles;     // row-tiled kernels: blocks across one row (set at launch)
     int64_t fper;          // logical blocks per front (set at launch)
+    int32_t block_threads; // the launch's block width (set at launch): read from the
+                           // arguments, since blockDim.x costs a vector load per wave
 };
 
 // Grid of nblocks blocks. A dispatch counts work-items in 32 bits per grid
