@@ -369,6 +369,23 @@ void test_host_f16_conversion() {
     std::printf("    f16 / bf16 storage conversions equal the oracle's (%zu values)\n", xs.size());
 }
 
+// The argument checks that come before any device call, with the reference's
+// messages (modules/nn.mojo:588-647; modules/rope.mojo:24-37;
+// sparse/basic.mojo:89-104) and the library's own for a host-side failure.
+void test_host_errors() {
+    expect_error([] { nn::activation(Tensor(), 7); }, "unknown activation");
+    expect_error([] { nn::RotaryPositionEmbedder(63); }, "RotaryPositionEmbedder: head_dim must be even");
+    expect_error([] { sp::SparseRotaryPositionEmbedder(63); }, "SparseRotaryPositionEmbedder: head_dim must be even");
+    expect_error([] { nn::rope_freqs(7); }, "head_dim");
+    expect_error([] { sp::VarLenTensor(Tensor(), {0, 3, 2, 5}); }, "VarLenTensor: invalid offsets");
+    expect_error([] { Tensor::from_values({2, 2}, {1, 2, 3}); }, "Tensor.from_values: size mismatch");
+    const std::vector<float> f = nn::rope_freqs(128);
+    std::vector<float> want(64);
+    EXPECT(orc_rope_freqs(128, 3, 1.0, 10000.0, want.data()) == (int64_t)f.size());
+    EXPECT(std::memcmp(f.data(), want.data(), f.size() * 4) == 0);
+    std::printf("    argument errors raise t2h::Error with the reference's messages\n");
+}
+
 void test_abi_errors_propagate() {
     // a status from libt2h arrives as t2h::Error with the library's message
     expect_error([] { nn::rope_freqs(7); }, "head_dim");
@@ -395,15 +412,25 @@ int main(int argc, char** argv) {
         {"abi_errors_propagate", test_abi_errors_propagate},
     };
     if (argc > 1 && std::strcmp(argv[1], "--host") == 0) {   // the checks that need no GPU
-        try {
-            std::printf("test host_f16_conversion\n");
-            test_host_f16_conversion();
-            std::printf("ok host_f16_conversion\n");
-            return 0;
-        } catch (const Failure& f) {
-            std::printf("FAIL host_f16_conversion: %s\n", f.what.c_str());
-            return 1;
+        const std::vector<std::pair<const char*, std::function<void()>>> host_tests = {
+            {"host_f16_conversion", test_host_f16_conversion},
+            {"host_errors", test_host_errors},
+        };
+        int failed = 0;
+        for (const auto& t : host_tests) {
+            std::printf("test %s\n", t.first);
+            try {
+                t.second();
+                std::printf("ok %s\n", t.first);
+            } catch (const Failure& f) {
+                ++failed;
+                std::printf("FAIL %s: %s\n", t.first, f.what.c_str());
+            } catch (const std::exception& e) {
+                ++failed;
+                std::printf("FAIL %s: unexpected exception: %s\n", t.first, e.what());
+            }
         }
+        return failed == 0 ? 0 : 1;
     }
     const char* filter = argc > 1 ? argv[1] : nullptr;
     if (t2h_device_init(0) != T2H_OK) {

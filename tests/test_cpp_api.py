@@ -3,9 +3,10 @@ test program tests/cpp/test_t2h_cpp (built by __graft_entry__.build() with
 tests/cpp/Makefile): the reference's tests/parity/test_sparse_basic.mojo
 cases and the oracle parity of each op, through the header's classes.
 
-The CPU test runs the header's host-side checks (f16 / bf16 storage
-conversion against the oracle); the GPU test runs the whole program, one
-process, and reports each case it ran."""
+The CPU test runs the header's host-side checks: the f16 / bf16 storage
+conversion against the oracle, and the argument errors raised before any
+device call. The GPU test runs the whole program, one process, and reports
+each case it ran."""
 import os
 import subprocess
 
@@ -31,7 +32,7 @@ def _run(args, timeout):
 def test_cpp_header_host_conversions():
     p = _run(["--host"], 60)
     assert p.returncode == 0, p.stdout[-2000:]
-    assert "ok host_f16_conversion" in p.stdout
+    assert "ok host_f16_conversion" in p.stdout and "ok host_errors" in p.stdout
 
 
 @pytest.mark.gpu
