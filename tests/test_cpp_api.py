@@ -22,6 +22,21 @@ def _binary() -> str:
     return BINARY
 
 
+def _build_if_missing() -> None:
+    """On the CPU, build the program (and the two libraries it links) when a
+    fresh tree has none, as the other CPU tests do for libt2h and the oracle."""
+    if os.path.exists(BINARY):
+        return
+    import oracle as orc
+    from t2h import _build
+
+    if not os.path.exists(_build.LIB_PATH):
+        _build.build()
+    orc.build()
+    subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True, stdout=subprocess.PIPE,
+                   stderr=subprocess.STDOUT)
+
+
 def _run(args, timeout):
     p = subprocess.run([_binary(), *args], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
                        timeout=timeout)
@@ -30,6 +45,7 @@ def _run(args, timeout):
 
 
 def test_cpp_header_host_conversions():
+    _build_if_missing()
     p = _run(["--host"], 60)
     assert p.returncode == 0, p.stdout[-2000:]
     assert "ok host_f16_conversion" in p.stdout and "ok host_errors" in p.stdout
