@@ -97,3 +97,40 @@ def test_oracle_not_linked(lib):
 
     out = subprocess.run(["readelf", "-d", _build.LIB_PATH], stdout=subprocess.PIPE, text=True).stdout
     assert "oracle" not in out
+
+
+def test_last_error_is_per_thread(lib):
+    """t2h_last_error() is thread-local: each thread reads the message of its
+    own last call, whatever the others did in between, and a successful call
+    clears only its own thread's message."""
+    import threading
+
+    p = ctypes.c_void_p(16)
+    n = 8
+    barrier = threading.Barrier(n)
+    results = {}
+
+    def worker(i):
+        if i % 2:
+            rc = lib.t2h_activation(p, p, None, 4, 8, 0, 9, None)
+            want = b"unknown activation"
+        else:
+            rc = lib.t2h_ln_modulate(p, p, 4, 1536, 7, 1e-6, 0, None, None, 0, None, 1, 0, None)
+            want = b"bad dtype"
+        barrier.wait()   # every thread has failed its call before any reads its message
+        own = lib.t2h_last_error()
+        barrier.wait()
+        if i == 0:
+            assert lib.t2h_activation(None, None, None, 0, 8, 0, 3, None) == 0   # rows 0: success
+        barrier.wait()
+        results[i] = (rc, own, lib.t2h_last_error(), want)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(n)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(results) == n
+    for i, (rc, own, after, want) in results.items():
+        assert rc == _lib.T2H_EINVAL and want in own, (i, own)
+        assert after == (b"" if i == 0 else own), (i, after)
