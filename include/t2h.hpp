@@ -20,6 +20,11 @@
 //   sparse::Modulation         sparse/transformer/modulated.mojo:24-57
 //   sparse::SparseRotaryPositionEmbedder
 //                              sparse/attention/rope.mojo:20-134
+//   block::pack_block_consts, block::cross_block_enqueue
+//                              gpu/block.mojo:217-397 (const layout 255-289)
+//   block::ModulatedCrossBlock modules/transformer/modulated.mojo:177-200,
+//                              sparse/transformer/modulated.mojo:187-226
+//   samplers::FlowEulerSampler samplers/flow_euler.mojo:62-264
 //
 // Calls run on the default HIP stream and are ordered with each other; a
 // host read (Tensor::to_host, the SparseTensor layout check) synchronises.
@@ -34,6 +39,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -184,6 +190,13 @@ public:
         return out;
     }
 
+    // A new tensor with a copy of the values (the reference's Tensor.copy()).
+    Tensor clone() const {
+        Tensor t = empty(shape_, dtype_);
+        if (numel() > 0) check_hip(hipMemcpy(t.data(), data(), bytes(), hipMemcpyDeviceToDevice), "hipMemcpy");
+        return t;
+    }
+
     // Same storage, another shape of the same size.
     Tensor reshape(std::vector<int64_t> shape) const {
         if (detail::product(shape) != numel()) throw Error("Tensor.reshape: size mismatch");
@@ -201,6 +214,8 @@ public:
     size_t bytes() const { return (size_t)numel() * dtype_size(dtype_); }
     DType dtype() const { return dtype_; }
     void* data() const { return buf_.get(); }
+    // false for a default-constructed Tensor (an absent optional argument)
+    bool defined() const { return static_cast<bool>(buf_) || !shape_.empty(); }
 
 private:
     std::shared_ptr<void> buf_;
@@ -658,6 +673,306 @@ struct SparseRotaryPositionEmbedder {
 };
 
 }  // namespace sparse
+
+// ---- the cross block's per-token glue: gpu/block.mojo:217-397,
+// modules/transformer/modulated.mojo:177-200, sparse/transformer/modulated.mojo:187-226
+namespace block {
+
+// A block's GEMM / attention work, outside this library: takes the normed
+// rows [T, C] and returns a new tensor of the same shape and dtype.
+using Chain = std::function<Tensor(const Tensor&)>;
+
+// const-buffer pair offsets in units of C (gpu/block.mojo:255-262)
+constexpr int BK_NORM1 = 0;        // shift1, scale1           (norm1 modulate)
+constexpr int BK_SELF_JOIN = 2;    // self_out bias, gate1     (self residual join)
+constexpr int BK_NORM2 = 4;        // norm2 weight, bias       (affine norm2)
+constexpr int BK_CROSS_JOIN = 6;   // cross_out bias, 0        (ungated cross join)
+constexpr int BK_NORM3 = 8;        // shift3, scale3           (norm3 modulate)
+constexpr int BK_MLP_JOIN = 10;    // mlp2 bias, gate3         (mlp residual join)
+constexpr int BK_FLOATS = 12;      // buffer size in units of C
+
+// The block's glue consts [12C] f32 in the reference's layout
+// (gpu/block.mojo:255-289). m = the six adaLN chunks of one batch row
+// (shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp); an absent
+// out bias (a default Tensor) is zeros, as in the reference.
+inline Tensor pack_block_consts(const std::vector<Tensor>& m, const Tensor& norm2_weight, const Tensor& norm2_bias,
+                                const Tensor& self_out_bias = Tensor(), const Tensor& cross_out_bias = Tensor(),
+                                const Tensor& mlp2_bias = Tensor()) {
+    if (m.size() != 6) throw Error("gpu_cross_block_enqueue: expected 6 mod chunks");
+    const int64_t c = m[0].numel();
+    const Tensor* parts[BK_FLOATS] = {&m[0], &m[1], &self_out_bias, &m[2], &norm2_weight, &norm2_bias,
+                                      &cross_out_bias, nullptr, &m[3], &m[4], &mlp2_bias, &m[5]};
+    Tensor bk = Tensor::zeros({BK_FLOATS * c});
+    for (int i = 0; i < BK_FLOATS; ++i) {
+        if (parts[i] == nullptr || !parts[i]->defined()) continue;
+        if (parts[i]->numel() != c || parts[i]->dtype() != F32)
+            throw Error("pack_block_consts: every part must be " + std::to_string(c) + " float32 values");
+        check_hip(hipMemcpy(static_cast<float*>(bk.data()) + i * c, parts[i]->data(), (size_t)c * 4,
+                            hipMemcpyDeviceToDevice),
+                  "hipMemcpy");
+    }
+    return bk;
+}
+
+namespace detail {
+
+inline Tensor chain_out(const Chain& chain, const Tensor& in, const Tensor& like, const char* what) {
+    Tensor h = chain(in);
+    if (h.shape() != like.shape() || h.dtype() != like.dtype())
+        throw Error(std::string("cross_block_enqueue: ") + what + " chain returned a tensor of another shape or dtype");
+    return h;
+}
+
+}  // namespace detail
+
+// One block against the resident rows xs [rows, C], updated in place and
+// returned, in the order of gpu/block.mojo:304-397:
+//   hs = LN(xs)*(1+scale1)+shift1;        h = self_chain(hs)
+//   xs += (h + self_out_bias) * gate1;    hs = LN(xs)*w2 + b2
+//   h = cross_chain(hs);                  xs += h + cross_out_bias
+//   hs = LN(xs)*(1+scale3)+shift3;        h = mlp_chain(hs)
+//   xs += (h + mlp2_bias) * gate3
+// The chains return their output without the out-linear bias, which the
+// joins fold in, as the reference's do. fused: each join and the next norm
+// in one pass (t2h_block_join_ln).
+inline Tensor& cross_block_enqueue(Tensor& xs, const Tensor& bk, const Chain& self_chain, const Chain& cross_chain,
+                                   const Chain& mlp_chain, bool fused = true) {
+    if (xs.ndim() != 2) throw Error("cross_block_enqueue: xs must be [rows, C]");
+    const int64_t rows = xs.dim(0), c = xs.dim(1);
+    if (bk.numel() != BK_FLOATS * c || bk.dtype() != F32)
+        throw Error("cross_block_enqueue: consts must hold " + std::to_string(BK_FLOATS * c) + " floats");
+    const float* k = static_cast<const float*>(bk.data());
+    const int32_t ci = (int32_t)c;
+    const DType dt = xs.dtype();
+    Tensor hs = Tensor::empty(xs.shape(), dt);
+    check(t2h_ln_mod_rows(xs.data(), hs.data(), k, rows, ci, BK_NORM1 * ci, 1, dt, nullptr));
+    Tensor h = detail::chain_out(self_chain, hs, xs, "self");
+    if (h.data() == hs.data()) hs = Tensor::empty(xs.shape(), dt);   // the chain handed back its input
+    if (fused) {
+        check(t2h_block_join_ln(xs.data(), h.data(), hs.data(), k, rows, ci, BK_SELF_JOIN * ci, 1, BK_NORM2 * ci, 2,
+                                dt, nullptr));
+    } else {
+        check(t2h_gate_add_bias_rows(xs.data(), h.data(), k, rows, ci, BK_SELF_JOIN * ci, 1, dt, nullptr));
+        check(t2h_ln_mod_rows(xs.data(), hs.data(), k, rows, ci, BK_NORM2 * ci, 2, dt, nullptr));
+    }
+    h = detail::chain_out(cross_chain, hs, xs, "cross");
+    if (h.data() == hs.data()) hs = Tensor::empty(xs.shape(), dt);
+    if (fused) {
+        check(t2h_block_join_ln(xs.data(), h.data(), hs.data(), k, rows, ci, BK_CROSS_JOIN * ci, 0, BK_NORM3 * ci, 1,
+                                dt, nullptr));
+    } else {
+        check(t2h_gate_add_bias_rows(xs.data(), h.data(), k, rows, ci, BK_CROSS_JOIN * ci, 0, dt, nullptr));
+        check(t2h_ln_mod_rows(xs.data(), hs.data(), k, rows, ci, BK_NORM3 * ci, 1, dt, nullptr));
+    }
+    h = detail::chain_out(mlp_chain, hs, xs, "mlp");
+    check(t2h_gate_add_bias_rows(xs.data(), h.data(), k, rows, ci, BK_MLP_JOIN * ci, 1, dt, nullptr));
+    return xs;
+}
+
+// The glue of ModulatedTransformerCrossBlock / ModulatedSparseTransformerCrossBlock:
+// norm1 and norm3 non-affine, norm2 affine, all with eps (1e-6 in the DiT
+// blocks, loaders.mojo:53-60). `modulation` is the share_mod parameter [6C]
+// (Modulation), or absent when `mod` already holds the chunks [B, 6C]. The
+// chains return complete outputs (bias included), as the reference's
+// attention modules do; each row reads its batch's adaLN chunk in place.
+class ModulatedCrossBlock {
+public:
+    ModulatedCrossBlock(int64_t channels, Tensor norm2_weight, Tensor norm2_bias, Tensor modulation = Tensor(),
+                        double eps = 1e-6)
+        : c_(channels), eps_((float)eps), w2_(std::move(norm2_weight)), b2_(std::move(norm2_bias)),
+          modulation_(std::move(modulation)) {
+        if (w2_.numel() != c_ || b2_.numel() != c_ || w2_.dtype() != F32 || b2_.dtype() != F32)
+            throw Error("ModulatedCrossBlock: norm2 weight and bias must be [C] float32");
+    }
+
+    // dense x [N, L, C], mod [N, 6C] (or [N, C] with the share_mod parameter's 6C added)
+    Tensor forward(const Tensor& x, const Tensor& mod, const Chain& self_attn, const Chain& cross_attn,
+                   const Chain& mlp) const {
+        if (x.ndim() != 3 || x.dim(2) != c_) throw Error("LayerNorm32: last dim mismatch");
+        const Tensor m = chunks(mod);
+        if (m.dim(0) != x.dim(0)) throw Error("modulate: shift/scale shape mismatch");
+        const Tensor out = run(x.reshape({x.dim(0) * x.dim(1), c_}), m, nullptr, (int32_t)x.dim(0), x.dim(1),
+                               self_attn, cross_attn, mlp);
+        return out.reshape(x.shape());
+    }
+
+    // sparse feats [T, C], mod [B, 6C]
+    sparse::SparseTensor forward(const sparse::SparseTensor& x, const Tensor& mod, const Chain& self_attn,
+                                 const Chain& cross_attn, const Chain& mlp) const {
+        if (x.feats.ndim() != 2 || x.feats.dim(1) != c_) throw Error("LayerNorm32: last dim mismatch");
+        const Tensor m = chunks(mod);
+        if (m.dim(0) != x.batch_size()) throw Error("SparseTensor.elemwise_batch: batch size mismatch");
+        return x.replace(run(x.feats, m, x.device_offsets(), (int32_t)x.batch_size(), 0, self_attn, cross_attn, mlp));
+    }
+
+private:
+    // mod [B, 6C] f32, plus the share_mod parameter when there is one
+    // (sparse/transformer/modulated.mojo:41-48)
+    Tensor chunks(const Tensor& mod) const {
+        if (mod.ndim() != 2 || mod.dim(1) != 6 * c_ || mod.dtype() != F32)
+            throw Error("ModulatedCrossBlock: mod must be [B, 6C] float32");
+        if (!modulation_.defined()) return mod;
+        Tensor m = Tensor::empty(mod.shape());
+        check(t2h_modulation_add(static_cast<const float*>(mod.data()), t2h::detail::f32_ptr(modulation_, "Modulation"),
+                                 static_cast<float*>(m.data()), mod.dim(0), 6 * c_, nullptr));
+        return m;
+    }
+
+    Tensor run(const Tensor& feats, const Tensor& m6, const int64_t* offsets, int32_t nbatch, int64_t rows_per_batch,
+               const Chain& self_attn, const Chain& cross_attn, const Chain& mlp) const {
+        const int64_t rows = feats.dim(0), ps = 6 * c_;
+        const int32_t ci = (int32_t)c_;
+        const DType dt = feats.dtype();
+        const float* m = static_cast<const float*>(m6.data());   // chunk i of batch b at m + b * 6C + i * C
+        const float* w2 = static_cast<const float*>(w2_.data());
+        const float* b2 = static_cast<const float*>(b2_.data());
+        // h = modulate(norm1(x), shift_msa, scale_msa)
+        Tensor h = Tensor::empty(feats.shape(), dt);
+        check(t2h_ln_modulate(feats.data(), h.data(), rows, ci, dt, eps_, T2H_LN_MODULATE, m, m + c_, ps, offsets,
+                              nbatch, rows_per_batch, nullptr));
+        h = detail::chain_out(self_attn, h, feats, "self");
+        // y = x + h * gate_msa;  h2 = norm2(y) (affine)
+        Tensor y = Tensor::empty(feats.shape(), dt), h2 = Tensor::empty(feats.shape(), dt);
+        check(t2h_gate_residual_ln_modulate(feats.data(), h.data(), y.data(), h2.data(), nullptr, m + 2 * c_, ps, eps_,
+                                            T2H_LN_AFFINE, w2, b2, 0, rows, ci, dt, offsets, nbatch, rows_per_batch,
+                                            nullptr));
+        h2 = detail::chain_out(cross_attn, h2, feats, "cross");
+        // y = y + h2;  h3 = modulate(norm3(y), shift_mlp, scale_mlp)
+        Tensor h3 = Tensor::empty(feats.shape(), dt);
+        check(t2h_gate_residual_ln_modulate(y.data(), h2.data(), y.data(), h3.data(), nullptr, nullptr, 0, eps_,
+                                            T2H_LN_MODULATE, m + 3 * c_, m + 4 * c_, ps, rows, ci, dt, offsets, nbatch,
+                                            rows_per_batch, nullptr));
+        h3 = detail::chain_out(mlp, h3, feats, "mlp");
+        // y = y + h3 * gate_mlp
+        check(t2h_gate_residual(y.data(), h3.data(), y.data(), nullptr, m + 5 * c_, ps, rows, ci, dt, offsets, nbatch,
+                                rows_per_batch, nullptr));
+        return y;
+    }
+
+    int64_t c_;
+    float eps_;
+    Tensor w2_, b2_, modulation_;
+};
+
+}  // namespace block
+
+// ---- samplers/flow_euler.mojo -------------------------------------------------------
+namespace samplers {
+
+constexpr int GUIDANCE_NONE = 0, GUIDANCE_CFG = 1, GUIDANCE_CFG_INTERVAL = 2;   // flow_euler.mojo:27-29
+
+// The velocity model (the DiT, outside this library): model(x_t, t * 1000,
+// use_neg_cond) returns a tensor of x_t's shape and dtype.
+using Model = std::function<Tensor(const Tensor& x_t, double t1000, bool use_neg_cond)>;
+
+// np.linspace(1, 0, steps + 1) rescaled: rescale_t*t / (1 + (rescale_t-1)*t)
+// (flow_euler.mojo:195-198), in f64.
+inline std::vector<double> t_schedule(int steps, double rescale_t) {
+    std::vector<double> out;
+    for (int i = 0; i <= steps; ++i) {
+        const double t = 1.0 - (double)i / (double)steps;
+        out.push_back(rescale_t * t / (1.0 + (rescale_t - 1.0) * t));
+    }
+    return out;
+}
+
+// The edict FlowEulerSampler.sample returns (flow_euler.mojo:44-53).
+struct SampleResult {
+    Tensor samples;
+    std::vector<Tensor> pred_x_t, pred_x_0;
+};
+
+// FlowEulerSampler / FlowEulerCfgSampler / FlowEulerGuidanceIntervalSampler
+// (flow_euler.mojo:62-264). The step schedule and the guidance decisions stay
+// on the host in f64, as in the reference; each step's tensor math (CFG
+// combine, CFG rescale, Euler update, x_0 prediction) is one
+// t2h_flow_euler_step call. The rescale's workspace is kept between steps.
+class FlowEulerSampler {
+public:
+    explicit FlowEulerSampler(double sigma_min) : sigma_min_(sigma_min) {}
+
+    // One step: {x_prev, pred_x0} from the predictions (v_neg null: none).
+    // seg_offsets: the varlen token segments (per-segment biased std in the
+    // rescale); empty: one segment per row.
+    std::pair<Tensor, Tensor> step(const Tensor& x_t, const Tensor& v_pos, const Tensor* v_neg, double t, double t_prev,
+                                   double guidance_strength = 1.0, double guidance_rescale = 0.0,
+                                   const std::vector<int64_t>& seg_offsets = {}) {
+        if (v_pos.shape() != x_t.shape() || v_pos.dtype() != x_t.dtype() ||
+            (v_neg != nullptr && (v_neg->shape() != x_t.shape() || v_neg->dtype() != x_t.dtype())))
+            throw Error("FlowEulerSampler: predictions must match x_t");
+        const int64_t rows = x_t.rows(), rs = x_t.row_size();
+        Tensor x_prev = Tensor::empty(x_t.shape(), x_t.dtype()), x0 = Tensor::empty(x_t.shape(), x_t.dtype());
+        void* ws = nullptr;
+        int64_t ws_bytes = 0;
+        if (v_neg != nullptr && guidance_rescale > 0.0) {
+            const int64_t need = t2h_flow_euler_workspace(rows, rs, (int32_t)seg_offsets.size());
+            if (need > ws_bytes_) {
+                ws_ = t2h::detail::device_alloc((size_t)need);
+                ws_bytes_ = need;
+            }
+            ws = ws_.get();
+            ws_bytes = ws_bytes_;
+        }
+        check(t2h_flow_euler_step(x_t.data(), v_pos.data(), v_neg != nullptr ? v_neg->data() : nullptr, x_prev.data(),
+                                  x0.data(), rows, rs, x_t.dtype(), t, t_prev, sigma_min_, guidance_strength,
+                                  guidance_rescale, seg_offsets.empty() ? nullptr : seg_offsets.data(),
+                                  (int32_t)seg_offsets.size(), ws, ws_bytes, nullptr));
+        return {x_prev, x0};
+    }
+
+    SampleResult sample(const Model& model, const Tensor& noise, int steps = 50, double rescale_t = 1.0) {
+        return sample_impl(model, noise, steps, rescale_t, GUIDANCE_NONE, 1.0, 0.0, 1.0, 0.0, {});
+    }
+    SampleResult sample_cfg(const Model& model, const Tensor& noise, int steps = 50, double rescale_t = 1.0,
+                            double guidance_strength = 3.0, double guidance_rescale = 0.0,
+                            const std::vector<int64_t>& seg_offsets = {}) {
+        return sample_impl(model, noise, steps, rescale_t, GUIDANCE_CFG, guidance_strength, 0.0, 1.0,
+                           guidance_rescale, seg_offsets);
+    }
+    SampleResult sample_cfg_interval(const Model& model, const Tensor& noise, int steps = 50, double rescale_t = 1.0,
+                                     double guidance_strength = 3.0, double interval_lo = 0.0,
+                                     double interval_hi = 1.0, double guidance_rescale = 0.0,
+                                     const std::vector<int64_t>& seg_offsets = {}) {
+        return sample_impl(model, noise, steps, rescale_t, GUIDANCE_CFG_INTERVAL, guidance_strength, interval_lo,
+                           interval_hi, guidance_rescale, seg_offsets);
+    }
+
+private:
+    // _sample_impl (flow_euler.mojo:183-214) with _inference's branches
+    // (151-181): the negative branch is evaluated only when it is used.
+    SampleResult sample_impl(const Model& model, const Tensor& noise, int steps, double rescale_t, int mode, double g,
+                             double lo, double hi, double gr, const std::vector<int64_t>& seg_offsets) {
+        Tensor x = noise.clone();
+        const std::vector<double> ts = t_schedule(steps, rescale_t);
+        SampleResult ret;
+        for (int i = 0; i < steps; ++i) {
+            const double t = ts[(size_t)i], tp = ts[(size_t)i + 1];
+            bool use_cfg = mode == GUIDANCE_CFG;
+            if (mode == GUIDANCE_CFG_INTERVAL) use_cfg = lo <= t && t <= hi;
+            std::pair<Tensor, Tensor> r;
+            if (!use_cfg || g == 1.0) {
+                r = step(x, model(x, 1000.0 * t, false), nullptr, t, tp, 1.0, gr, seg_offsets);
+            } else if (g == 0.0) {
+                r = step(x, model(x, 1000.0 * t, true), nullptr, t, tp, 1.0, gr, seg_offsets);
+            } else {
+                const Tensor pos = model(x, 1000.0 * t, false);
+                const Tensor neg = model(x, 1000.0 * t, true);
+                r = step(x, pos, &neg, t, tp, g, gr, seg_offsets);
+            }
+            x = r.first;
+            ret.pred_x_t.push_back(r.first);
+            ret.pred_x_0.push_back(r.second);
+        }
+        ret.samples = x;
+        return ret;
+    }
+
+    double sigma_min_;
+    std::shared_ptr<void> ws_;
+    int64_t ws_bytes_ = 0;
+};
+
+}  // namespace samplers
 }  // namespace t2h
 
 #endif  // T2H_HPP

@@ -329,6 +329,225 @@ void test_modulation_chunks() {
     expect_error([&] { m.chunks(Tensor::zeros({n, 5 * c}), c); }, "Modulation: expected [N, 6C] modulation rows");
 }
 
+// ---- the cross block's glue (modules/transformer/modulated.mojo:177-200,
+// sparse/transformer/modulated.mojo:187-226, gpu/block.mojo:217-397) ---------------
+namespace blk = t2h::block;
+
+// Device chains built from bit-exact elementwise ops, so that the host side
+// repeats them exactly: self h * 0.5, cross h + 0.25, mlp h * -0.75.
+Tensor scaled(const Tensor& h, float v, int op) {
+    const int64_t rows = h.rows();
+    return sp::VarLenTensor(h, {0, rows}).elemwise_scalar(v, op).feats;
+}
+std::vector<float> host_scaled(const std::vector<float>& h, float v, int op) {
+    std::vector<float> o(h.size());
+    orc_binop_scalar(h.data(), v, o.data(), (int64_t)h.size(), op, 0);
+    return o;
+}
+
+// host: LN (non-affine, or affine with w/b) over rows of c
+std::vector<float> host_ln(const std::vector<float>& x, int64_t c, const float* w = nullptr, const float* b = nullptr) {
+    std::vector<float> o(x.size());
+    orc_layernorm(x.data(), o.data(), (int64_t)x.size() / c, c, 1e-6, w != nullptr, w, b);
+    return o;
+}
+// host: fl(h * gate[b(r)]) added to x, with gate rows [B, C] and the batch offsets
+std::vector<float> host_gated_add(const std::vector<float>& x, const std::vector<float>& h, const float* gate_rows,
+                                  const std::vector<int64_t>& offsets, int64_t c) {
+    const int64_t rows = (int64_t)x.size() / c, nb = (int64_t)offsets.size() - 1;
+    std::vector<int64_t> map((size_t)rows);
+    orc_batch_broadcast_map(offsets.data(), nb, map.data());
+    std::vector<float> t(x.size()), o(x.size());
+    orc_binop_rows(h.data(), gate_rows, map.data(), t.data(), rows, c, c, sp::OP_MUL);
+    orc_binop_flat(x.data(), t.data(), o.data(), (int64_t)x.size(), sp::OP_ADD);
+    return o;
+}
+// the rows of chunk i of a [B, 6C] modulation: [B, C]
+std::vector<float> chunk_rows(const std::vector<float>& m6, int64_t nb, int64_t c, int i) {
+    std::vector<float> o((size_t)(nb * c));
+    for (int64_t b = 0; b < nb; ++b) std::memcpy(&o[(size_t)(b * c)], &m6[(size_t)(b * 6 * c + i * c)], (size_t)c * 4);
+    return o;
+}
+
+// The host composition of ModulatedCrossBlock.forward with the chains above.
+std::vector<float> host_block(const std::vector<float>& x, const std::vector<float>& m6, const std::vector<float>& w2,
+                              const std::vector<float>& b2, const std::vector<int64_t>& offsets, int64_t c) {
+    const int64_t rows = (int64_t)x.size() / c, nb = (int64_t)offsets.size() - 1;
+    auto mod = [&](const std::vector<float>& v, int i_shift, int i_scale) {
+        const auto sh = chunk_rows(m6, nb, c, i_shift), sc = chunk_rows(m6, nb, c, i_scale);
+        std::vector<float> o(v.size());
+        orc_mod_shift_scale(v.data(), sh.data(), sc.data(), offsets.data(), nb, o.data(), rows, c);
+        return o;
+    };
+    auto h = host_scaled(mod(host_ln(x, c), 0, 1), 0.5f, sp::OP_MUL);
+    auto y = host_gated_add(x, h, chunk_rows(m6, nb, c, 2).data(), offsets, c);
+    auto h2 = host_scaled(host_ln(y, c, w2.data(), b2.data()), 0.25f, sp::OP_ADD);
+    std::vector<float> y2(y.size());
+    orc_binop_flat(y.data(), h2.data(), y2.data(), (int64_t)y.size(), sp::OP_ADD);
+    auto h3 = host_scaled(mod(host_ln(y2, c), 3, 4), -0.75f, sp::OP_MUL);
+    return host_gated_add(y2, h3, chunk_rows(m6, nb, c, 5).data(), offsets, c);
+}
+
+void test_modulated_cross_block() {
+    const int64_t n = 2, l = 37, c = 1536;
+    const auto x = randn(41, n * l * c), mod = randn(42, n * 6 * c, 0.1), par = randn(43, 6 * c, 0.02);
+    const auto w2 = randn(44, c, 0.1), b2 = randn(45, c, 0.1);
+    std::vector<float> m6((size_t)(n * 6 * c));
+    orc_modulation_add(mod.data(), par.data(), m6.data(), n, 6 * c);
+    const blk::ModulatedCrossBlock block(c, Tensor::from_host(w2.data(), {c}), Tensor::from_host(b2.data(), {c}),
+                                         Tensor::from_host(par.data(), {6 * c}), 1e-6);
+    const blk::Chain self_attn = [](const Tensor& h) { return scaled(h, 0.5f, sp::OP_MUL); };
+    const blk::Chain cross_attn = [](const Tensor& h) { return scaled(h, 0.25f, sp::OP_ADD); };
+    const blk::Chain mlp = [](const Tensor& h) { return scaled(h, -0.75f, sp::OP_MUL); };
+    const Tensor modd = Tensor::from_host(mod.data(), {n, 6 * c});
+    // dense [N, L, C]: batch b owns rows [b L, (b + 1) L)
+    const Tensor out = block.forward(Tensor::from_host(x.data(), {n, l, c}), modd, self_attn, cross_attn, mlp);
+    EXPECT((out.shape() == std::vector<int64_t>{n, l, c}));
+    expect_close(out.to_host(), host_block(x, m6, w2, b2, {0, l, 2 * l}, c), 1e-5, "ModulatedCrossBlock dense");
+    // sparse: three batches, the middle one empty
+    const int64_t rows = 90;
+    std::vector<int32_t> coords((size_t)rows * 4, 0);
+    for (int64_t r = 0; r < rows; ++r) coords[(size_t)r * 4] = r < 50 ? 0 : 2;
+    const auto xs = randn(46, rows * c), mods = randn(47, 3 * 6 * c, 0.1);
+    std::vector<float> m6s((size_t)(3 * 6 * c));
+    orc_modulation_add(mods.data(), par.data(), m6s.data(), 3, 6 * c);
+    const sp::SparseTensor st(Tensor::from_host(xs.data(), {rows, c}), IntMatrix::from_host(coords.data(), rows, 4), 3);
+    const auto so = block.forward(st, Tensor::from_host(mods.data(), {3, 6 * c}), self_attn, cross_attn, mlp);
+    expect_close(so.feats.to_host(), host_block(xs, m6s, w2, b2, {0, 50, 50, rows}, c), 1e-5,
+                 "ModulatedCrossBlock sparse");
+    expect_error([&] { block.forward(st, modd, self_attn, cross_attn, mlp); }, "batch size mismatch");
+    expect_error([&] { block.forward(Tensor::zeros({n, l, c - 8}), modd, self_attn, cross_attn, mlp); },
+                 "LayerNorm32: last dim mismatch");
+}
+
+void test_cross_block_enqueue() {
+    // the resident block over one const buffer; chains return no out bias
+    const int64_t rows = 77, c = 1536;
+    const auto x = randn(51, rows * c);
+    std::vector<Tensor> m;
+    std::vector<std::vector<float>> mh;
+    for (int i = 0; i < 6; ++i) {
+        mh.push_back(randn(52 + i, c, 0.1));
+        m.push_back(Tensor::from_host(mh.back().data(), {c}));
+    }
+    const auto w2 = randn(60, c, 0.1), b2 = randn(61, c, 0.1), bs = randn(62, c, 0.02), bc = randn(63, c, 0.02),
+               bm = randn(64, c, 0.02);
+    const Tensor bk = blk::pack_block_consts(m, Tensor::from_host(w2.data(), {c}), Tensor::from_host(b2.data(), {c}),
+                                             Tensor::from_host(bs.data(), {c}), Tensor::from_host(bc.data(), {c}),
+                                             Tensor::from_host(bm.data(), {c}));
+    const blk::Chain self_chain = [](const Tensor& h) { return scaled(h, 0.5f, sp::OP_MUL); };
+    const blk::Chain cross_chain = [](const Tensor& h) { return h; };   // hands back its input
+    const blk::Chain mlp_chain = [](const Tensor& h) { return scaled(h, -0.75f, sp::OP_MUL); };
+    Tensor xf = Tensor::from_host(x.data(), {rows, c}), xu = Tensor::from_host(x.data(), {rows, c});
+    blk::cross_block_enqueue(xf, bk, self_chain, cross_chain, mlp_chain, true);
+    blk::cross_block_enqueue(xu, bk, self_chain, cross_chain, mlp_chain, false);
+    const auto got = xf.to_host();
+    expect_bits(got, xu.to_host(), "cross_block_enqueue fused == unfused");
+    // host: the joins fold the out bias: x += fl(fl(h + bias) * gate)
+    const std::vector<int64_t> off{0, rows};
+    auto modulate = [&](const std::vector<float>& v, const std::vector<float>& sh, const std::vector<float>& sc) {
+        std::vector<float> o(v.size());
+        orc_mod_shift_scale(v.data(), sh.data(), sc.data(), off.data(), 1, o.data(), rows, c);
+        return o;
+    };
+    auto add_bias = [&](const std::vector<float>& v, const std::vector<float>& b) {
+        std::vector<float> o(v.size());
+        orc_add_bias(v.data(), b.data(), o.data(), rows, c);
+        return o;
+    };
+    auto h = host_scaled(modulate(host_ln(x, c), mh[0], mh[1]), 0.5f, sp::OP_MUL);
+    auto y = host_gated_add(x, add_bias(h, bs), mh[2].data(), off, c);
+    auto h2 = add_bias(host_ln(y, c, w2.data(), b2.data()), bc);
+    std::vector<float> y2(y.size());
+    orc_binop_flat(y.data(), h2.data(), y2.data(), (int64_t)y.size(), sp::OP_ADD);
+    auto h3 = host_scaled(modulate(host_ln(y2, c), mh[3], mh[4]), -0.75f, sp::OP_MUL);
+    expect_close(got, host_gated_add(y2, add_bias(h3, bm), mh[5].data(), off, c), 1e-5, "cross_block_enqueue");
+    expect_error([&] { blk::pack_block_consts({m[0]}, m[0], m[0]); }, "expected 6 mod chunks");
+}
+
+// ---- samplers/flow_euler.mojo --------------------------------------------------------
+namespace smp = t2h::samplers;
+
+void test_flow_euler_sampler() {
+    // t_schedule: t = 1 -> 1, t = 0 -> 0, rescale_t 1 is linspace(1, 0)
+    const auto ts1 = smp::t_schedule(4, 1.0);
+    EXPECT(ts1.size() == 5 && ts1[0] == 1.0 && ts1[2] == 0.5 && ts1[4] == 0.0);
+    const auto ts3 = smp::t_schedule(4, 3.0);
+    EXPECT(ts3[0] == 1.0 && ts3[4] == 0.0 && std::fabs(ts3[2] - 0.75) < 1e-15);   // 3 * 0.5 / (1 + 2 * 0.5)
+    // model: pos = fl(x * 0.75), neg = fl(fl(x * 0.25) + 0.5): bit-exact on both sides
+    const smp::Model model = [](const Tensor& x, double, bool neg) {
+        return neg ? scaled(scaled(x, 0.25f, sp::OP_MUL), 0.5f, sp::OP_ADD) : scaled(x, 0.75f, sp::OP_MUL);
+    };
+    auto host_model = [](const std::vector<float>& x, bool neg) {
+        return neg ? host_scaled(host_scaled(x, 0.25f, sp::OP_MUL), 0.5f, sp::OP_ADD) : host_scaled(x, 0.75f, sp::OP_MUL);
+    };
+    const int64_t rows = 64, rs = 32;
+    const double sigma_min = 1e-5;
+    const auto noise = randn(71, rows * rs);
+    struct Case {
+        const char* name;
+        int mode;
+        double g, lo, hi, gr;
+        std::vector<int64_t> seg;
+    };
+    const std::vector<Case> cases = {
+        {"sample", smp::GUIDANCE_NONE, 1.0, 0.0, 1.0, 0.0, {}},
+        {"sample_cfg", smp::GUIDANCE_CFG, 3.0, 0.0, 1.0, 0.0, {}},
+        {"sample_cfg rescale", smp::GUIDANCE_CFG, 3.0, 0.0, 1.0, 0.7, {}},
+        {"sample_cfg strength 0", smp::GUIDANCE_CFG, 0.0, 0.0, 1.0, 0.7, {}},
+        {"sample_cfg_interval rescale", smp::GUIDANCE_CFG_INTERVAL, 3.0, 0.3, 0.8, 0.7, {}},
+        {"sample_cfg varlen rescale", smp::GUIDANCE_CFG, 3.0, 0.0, 1.0, 0.7, {0, 20, 64}},
+    };
+    const int steps = 5;
+    const auto ts = smp::t_schedule(steps, 3.0);
+    for (const Case& k : cases) {
+        smp::FlowEulerSampler sampler(sigma_min);
+        const Tensor nd = Tensor::from_host(noise.data(), {rows, rs});
+        smp::SampleResult res;
+        if (k.mode == smp::GUIDANCE_NONE) res = sampler.sample(model, nd, steps, 3.0);
+        else if (k.mode == smp::GUIDANCE_CFG) res = sampler.sample_cfg(model, nd, steps, 3.0, k.g, k.gr, k.seg);
+        else res = sampler.sample_cfg_interval(model, nd, steps, 3.0, k.g, k.lo, k.hi, k.gr, k.seg);
+        EXPECT((int)res.pred_x_t.size() == steps && (int)res.pred_x_0.size() == steps);
+        // host: _inference's branches, then the Euler step (flow_euler.mojo:151-214)
+        std::vector<float> x = noise;
+        const bool rescaled = k.gr > 0.0;
+        const double tol = rescaled ? 1e-4 : 0.0;
+        for (int i = 0; i < steps; ++i) {
+            const double t = ts[(size_t)i], tp = ts[(size_t)i + 1];
+            bool use_cfg = k.mode == smp::GUIDANCE_CFG;
+            if (k.mode == smp::GUIDANCE_CFG_INTERVAL) use_cfg = k.lo <= t && t <= k.hi;
+            std::vector<float> v;
+            if (!use_cfg || k.g == 1.0) {
+                v = host_model(x, false);
+            } else if (k.g == 0.0) {
+                v = host_model(x, true);
+            } else {
+                const auto pos = host_model(x, false), neg = host_model(x, true);
+                v.resize(x.size());
+                orc_flow_cfg(pos.data(), neg.data(), v.data(), (int64_t)x.size(), k.g);
+                if (rescaled) {
+                    std::vector<float> r(x.size());
+                    orc_flow_rescale(x.data(), v.data(), pos.data(), r.data(), rows, rs, t, sigma_min, k.gr,
+                                     k.seg.empty() ? nullptr : k.seg.data(), (int64_t)k.seg.size());
+                    v = r;
+                }
+            }
+            std::vector<float> x0(x.size()), xn(x.size());
+            orc_flow_v_to_xstart(x.data(), v.data(), x0.data(), (int64_t)x.size(), t, sigma_min);
+            orc_flow_step(x.data(), v.data(), xn.data(), (int64_t)x.size(), t, tp);
+            x = xn;
+            if (tol == 0.0) {
+                expect_bits(res.pred_x_0[(size_t)i].to_host(), x0, k.name);
+                expect_bits(res.pred_x_t[(size_t)i].to_host(), x, k.name);
+            } else {
+                expect_close(res.pred_x_0[(size_t)i].to_host(), x0, tol, k.name);
+                expect_close(res.pred_x_t[(size_t)i].to_host(), x, tol, k.name);
+            }
+        }
+        EXPECT(std::memcmp(res.samples.to_host().data(), res.pred_x_t.back().to_host().data(), x.size() * 4) == 0);
+    }
+}
+
 // ---- host side of the header (no GPU) ------------------------------------------------
 bool same_value(float a, float b) {
     if (std::isnan(a) || std::isnan(b)) return std::isnan(a) && std::isnan(b);
@@ -409,6 +628,9 @@ int main(int argc, char** argv) {
         {"sparse_rope_embed", test_sparse_rope_embed},
         {"timestep_embedder", test_timestep_embedder},
         {"modulation_chunks", test_modulation_chunks},
+        {"modulated_cross_block", test_modulated_cross_block},
+        {"cross_block_enqueue", test_cross_block_enqueue},
+        {"flow_euler_sampler", test_flow_euler_sampler},
         {"abi_errors_propagate", test_abi_errors_propagate},
     };
     if (argc > 1 && std::strcmp(argv[1], "--host") == 0) {   // the checks that need no GPU
