@@ -503,7 +503,8 @@ public:
         return replace(detail::binop_rows(feats, v, o, nullptr, 1));
     }
     VarLenTensor operator+(const VarLenTensor& o) const {
-        if (o.feats.numel() != feats.numel()) throw Error("Tensor binop: size mismatch");
+        if (o.feats.numel() != feats.numel() || o.feats.dtype() != feats.dtype())
+            throw Error("Tensor binop: size mismatch");
         Tensor out = Tensor::empty(feats.shape(), feats.dtype());
         check(t2h_gate_residual(feats.data(), o.feats.data(), out.data(), nullptr, nullptr, 0, feats.rows(),
                                 (int32_t)feats.row_size(), feats.dtype(), nullptr, 1, 0, nullptr));
@@ -576,7 +577,8 @@ public:
     }
     // elementwise feats add (sparse/basic.mojo:438-439)
     SparseTensor operator+(const SparseTensor& o) const {
-        if (o.feats.numel() != feats.numel()) throw Error("Tensor binop: size mismatch");
+        if (o.feats.numel() != feats.numel() || o.feats.dtype() != feats.dtype())
+            throw Error("Tensor binop: size mismatch");
         Tensor out = Tensor::empty(feats.shape(), feats.dtype());
         check(t2h_gate_residual(feats.data(), o.feats.data(), out.data(), nullptr, nullptr, 0, feats.rows(),
                                 (int32_t)feats.row_size(), feats.dtype(), nullptr, 1, 0, nullptr));
