@@ -25,6 +25,10 @@
 //   block::ModulatedCrossBlock modules/transformer/modulated.mojo:177-200,
 //                              sparse/transformer/modulated.mojo:187-226
 //   samplers::FlowEulerSampler samplers/flow_euler.mojo:62-264
+//   gpu::linear, gpu::linear_gate_residual
+//                              gpu/linear.mojo:535-560, 662-684; gpu/block.mojo:86-110
+//   gpu::attn_pack, gpu::qkv_linear_pack
+//                              gpu/attention.mojo:507-662, 983-1013
 //
 // Calls run on the default HIP stream and are ordered with each other; a
 // host read (Tensor::to_host, the SparseTensor layout check) synchronises.
@@ -675,6 +679,151 @@ struct SparseRotaryPositionEmbedder {
 };
 
 }  // namespace sparse
+
+// ---- the device-resident chain's GEMM and attention operands: gpu/linear.mojo,
+// gpu/attention.mojo
+namespace gpu {
+
+namespace detail {
+
+inline const float* opt_f32(const Tensor& t, int64_t n, const char* what) {
+    if (!t.defined()) return nullptr;
+    if (t.dtype() != F32 || t.numel() != n)
+        throw Error(std::string(what) + ": must be " + std::to_string(n) + " float32 values");
+    return static_cast<const float*>(t.data());
+}
+
+inline void check_gemm(const Tensor& x, const Tensor& w, const char* what) {
+    if (x.ndim() != 2 || w.ndim() != 2 || x.dim(1) != w.dim(1) || x.dtype() != w.dtype() || x.dtype() == F32)
+        throw Error(std::string(what) + ": x [rows, K] and weight [N, K] must be float16 or bfloat16 alike");
+}
+
+}  // namespace detail
+
+// act(x @ weight^T + bias) on the matrix cores: GpuLinear.enqueue_gemm
+// (gpu/linear.mojo:535-560) with the bias and activation in the store (the
+// MLP's first linear + gelu_tanh_bias, 662-684). x [rows, K], weight [N, K]
+// in the checkpoint layout, both f16 or both bf16; bias [N] f32 or absent;
+// act a T2H_ACT_* kind or T2H_ACT_NONE; the output in out_dtype (F32 or x's).
+inline Tensor linear(const Tensor& x, const Tensor& weight, const Tensor& bias = Tensor(), int act = T2H_ACT_NONE,
+                     DType out_dtype = F32) {
+    detail::check_gemm(x, weight, "linear");
+    const int64_t rows = x.dim(0), k = x.dim(1), n = weight.dim(0);
+    Tensor out = Tensor::empty({rows, n}, out_dtype);
+    check(t2h_linear(x.data(), k, weight.data(), detail::opt_f32(bias, n, "linear: bias"), out.data(), n, rows,
+                     (int32_t)k, (int32_t)n, x.dtype(), out_dtype, act, nullptr));
+    return out;
+}
+
+// res + fl(fl(x @ weight^T + bias) * gate[b(r)]): an out-linear with the
+// block's gated residual join in its store (gpu/block.mojo:86-110;
+// sparse/transformer/modulated.mojo:214-226 for per-batch gate rows). gate
+// [B, N] or [N] f32, or absent (res + fl(acc + bias)); the batch map as in
+// t2h.h (offsets: device [B+1], or rows_per_batch). Returns a new tensor of
+// res's dtype (f32 or x's).
+inline Tensor linear_gate_residual(const Tensor& x, const Tensor& weight, const Tensor& res,
+                                   const Tensor& bias = Tensor(), const Tensor& gate = Tensor(),
+                                   const int64_t* offsets = nullptr, int32_t nbatch = 1,
+                                   int64_t rows_per_batch = 0) {
+    detail::check_gemm(x, weight, "linear_gate_residual");
+    const int64_t rows = x.dim(0), k = x.dim(1), n = weight.dim(0);
+    if (res.ndim() != 2 || res.dim(0) != rows || res.dim(1) != n || (res.dtype() != F32 && res.dtype() != x.dtype()))
+        throw Error("linear_gate_residual: res must be [rows, N] of x's dtype or float32");
+    if (gate.defined() && (gate.dtype() != F32 || gate.numel() != (int64_t)nbatch * n))
+        throw Error("linear_gate_residual: gate must be [B, N] float32");
+    Tensor out = Tensor::empty(res.shape(), res.dtype());
+    check(t2h_linear_gate_residual(x.data(), k, weight.data(), detail::opt_f32(bias, n, "linear_gate_residual: bias"),
+                                   res.data(), out.data(), n, rows, (int32_t)k, (int32_t)n, x.dtype(), res.dtype(),
+                                   gate.defined() ? static_cast<const float*>(gate.data()) : nullptr, n, offsets,
+                                   nbatch, rows_per_batch, nullptr));
+    return out;
+}
+
+// The attention operands of the self-attention chain (gpu/attention.mojo:
+// 566-594 pack_q_z, 634-662 pack_kv_z): qh [H, mp, D] = q * 1/sqrt(D),
+// k [H, D, lp] (the reference's transposed layout) or [H, lp, D] (row-major,
+// the faster one on MI355X), vh [H, lp, D]; rows past the tokens are zero.
+struct AttnOperands {
+    Tensor qh, k, vh;
+};
+
+// RoPE for the pack: the frequency table (empty: no RoPE) and the position
+// source, int32 voxel coords [rows, 1 + 3] or a dense grid of side grid_res.
+struct Rope {
+    std::vector<float> freqs;
+    const IntMatrix* coords = nullptr;
+    int32_t grid_res = 0;
+};
+
+namespace detail {
+
+struct PackOut {
+    AttnOperands o;
+    int64_t mp, lp;
+};
+
+inline PackOut pack_outputs(int64_t rows, int64_t heads, int64_t d, DType dt, int64_t mp, int64_t lp, bool kt) {
+    PackOut p;
+    p.mp = mp ? mp : rows;
+    p.lp = lp ? lp : rows;
+    p.o.qh = Tensor::empty({heads, p.mp, d}, dt);
+    p.o.k = kt ? Tensor::empty({heads, d, p.lp}, dt) : Tensor::empty({heads, p.lp, d}, dt);
+    p.o.vh = Tensor::empty({heads, p.lp, d}, dt);
+    return p;
+}
+
+}  // namespace detail
+
+// bias_rms_rope_qkv + pack_q_z + pack_kv_z (gpu/attention.mojo:507-563,
+// 566-594, 634-662; sequence 987-1013) in one pass over the qkv GEMM output
+// [rows, 3 * H * D]: +bias (q, k, v), RMS q and k (gammas [H, D]; absent:
+// no RMS), RoPE q and k, then the head-major pack.
+inline AttnOperands attn_pack(const Tensor& qkv, int32_t heads, const Tensor& bias, const Tensor& gamma_q,
+                              const Tensor& gamma_k, const Rope& rope = Rope(), int64_t mp = 0, int64_t lp = 0,
+                              bool k_transposed = true) {
+    if (qkv.ndim() != 2 || heads <= 0 || qkv.dim(1) % (3 * heads) != 0)
+        throw Error("attn_pack: qkv must be [rows, 3 * H * D]");
+    const int64_t rows = qkv.dim(0), hd = qkv.dim(1) / 3, d = hd / heads;
+    const DType dt = qkv.dtype();
+    detail::PackOut p = detail::pack_outputs(rows, heads, d, dt, mp, lp, k_transposed);
+    const char* q = static_cast<const char*>(qkv.data());
+    const size_t es = dtype_size(dt);
+    const float* b = detail::opt_f32(bias, 3 * hd, "attn_pack: bias");
+    check(t2h_attn_pack(q, q + hd * es, q + 2 * hd * es, 3 * hd, rows, heads, (int32_t)d, dt, b, b ? b + hd : nullptr,
+                        b ? b + 2 * hd : nullptr, detail::opt_f32(gamma_q, hd, "attn_pack: gamma_q"),
+                        detail::opt_f32(gamma_k, hd, "attn_pack: gamma_k"), rope.freqs.empty() ? 0 : 1,
+                        rope.freqs.empty() ? nullptr : rope.freqs.data(), (int32_t)rope.freqs.size(), 3, nullptr, 0,
+                        rope.coords ? rope.coords->data() : nullptr, rope.coords ? (int32_t)rope.coords->cols() : 0,
+                        rope.grid_res, p.o.qh.data(), p.mp, p.o.k.data(), p.o.vh.data(), p.lp, k_transposed ? 1 : 0,
+                        nullptr));
+    return p.o;
+}
+
+// The qkv linear on the matrix cores with attn_pack's epilogue and pack in
+// its store (gpu/attention.mojo:983-1013): x [rows, K], weight [3 * H * D, K]
+// (f16 or bf16), bias [3 * H * D] f32 or absent; the [rows, 3C] GEMM output
+// never reaches memory.
+inline AttnOperands qkv_linear_pack(const Tensor& x, const Tensor& weight, int32_t heads, const Tensor& bias,
+                                    const Tensor& gamma_q, const Tensor& gamma_k, const Rope& rope = Rope(),
+                                    int64_t mp = 0, int64_t lp = 0, bool k_transposed = true) {
+    detail::check_gemm(x, weight, "qkv_linear_pack");
+    if (heads <= 0 || weight.dim(0) % (3 * heads) != 0)
+        throw Error("qkv_linear_pack: weight rows must be 3 * heads * head_dim");
+    const int64_t rows = x.dim(0), k = x.dim(1), hd = weight.dim(0) / 3, d = hd / heads;
+    detail::PackOut p = detail::pack_outputs(rows, heads, d, x.dtype(), mp, lp, k_transposed);
+    const float* b = detail::opt_f32(bias, 3 * hd, "qkv_linear_pack: bias");
+    check(t2h_qkv_linear_pack(x.data(), k, weight.data(), rows, (int32_t)k, heads, (int32_t)d, x.dtype(), b,
+                              b ? b + hd : nullptr, b ? b + 2 * hd : nullptr,
+                              detail::opt_f32(gamma_q, hd, "qkv_linear_pack: gamma_q"),
+                              detail::opt_f32(gamma_k, hd, "qkv_linear_pack: gamma_k"), rope.freqs.empty() ? 0 : 1,
+                              rope.freqs.empty() ? nullptr : rope.freqs.data(), (int32_t)rope.freqs.size(), 3, nullptr,
+                              0, rope.coords ? rope.coords->data() : nullptr,
+                              rope.coords ? (int32_t)rope.coords->cols() : 0, rope.grid_res, p.o.qh.data(), p.mp,
+                              p.o.k.data(), p.o.vh.data(), p.lp, k_transposed ? 1 : 0, nullptr));
+    return p.o;
+}
+
+}  // namespace gpu
 
 // ---- the cross block's per-token glue: gpu/block.mojo:217-397,
 // modules/transformer/modulated.mojo:177-200, sparse/transformer/modulated.mojo:187-226

@@ -465,6 +465,127 @@ void test_cross_block_enqueue() {
     expect_error([&] { blk::pack_block_consts({m[0]}, m[0], m[0]); }, "expected 6 mod chunks");
 }
 
+// ---- gpu/linear.mojo, gpu/attention.mojo ---------------------------------------------
+namespace gp = t2h::gpu;
+
+// small integers in [-m, m]: exact in f16, their products and sums exact in f32
+std::vector<float> small_ints(uint64_t seed, int64_t n, int m) {
+    orc_rng r;
+    orc_rng_init(&r, seed);
+    std::vector<float> v((size_t)n);
+    for (auto& x : v) x = (float)((int)(orc_rng_next_u64(&r) % (uint64_t)(2 * m + 1)) - m);
+    return v;
+}
+
+std::vector<float> host_linear(const std::vector<float>& x, const std::vector<float>& w, int64_t rows, int64_t n,
+                               int64_t k) {
+    std::vector<float> c((size_t)(rows * n));
+    orc_linear(x.data(), w.data(), c.data(), rows, n, k, 4);
+    return c;
+}
+
+void test_gpu_linear() {
+    const int64_t rows = 100, k = 128, n = 256;
+    const auto x = small_ints(81, rows * k, 3), w = small_ints(82, n * k, 2), b = small_ints(83, n, 4);
+    const Tensor xd = Tensor::from_host(x.data(), {rows, k}, t2h::F16), wd = Tensor::from_host(w.data(), {n, k}, t2h::F16);
+    const Tensor bd = Tensor::from_host(b.data(), {n});
+    const auto acc = host_linear(x, w, rows, n, k);
+    std::vector<float> want(acc.size());
+    orc_add_bias(acc.data(), b.data(), want.data(), rows, n);
+    expect_bits(gp::linear(xd, wd, bd).to_host(), want, "linear f32 out (integer operands)");
+    expect_bits(gp::linear(xd, wd, bd, T2H_ACT_NONE, t2h::F16).to_host(), want, "linear f16 out (integer operands)");
+    std::vector<float> act(want.size());
+    EXPECT(orc_activation(want.data(), act.data(), (int64_t)want.size(), T2H_ACT_GELU_TANH, 1) == 0);
+    expect_close(gp::linear(xd, wd, bd, T2H_ACT_GELU_TANH).to_host(), act, 1e-5, "linear + GELU-tanh");
+    // the out-linear with the gated residual join, per-batch gate rows
+    const auto res = randn(84, rows * n), gate = randn(85, 2 * n, 0.1);
+    const std::vector<int64_t> off{0, 40, rows};
+    const sp::VarLenTensor batches(Tensor::zeros({rows, 1}), off);   // device offsets
+    const Tensor got = gp::linear_gate_residual(xd, wd, Tensor::from_host(res.data(), {rows, n}), bd,
+                                                Tensor::from_host(gate.data(), {2, n}), batches.device_offsets(), 2);
+    expect_bits(got.to_host(), host_gated_add(res, want, gate.data(), off, n), "linear_gate_residual");
+    expect_error([&] { gp::linear(xd, Tensor::from_host(w.data(), {n, k})); }, "float16 or bfloat16 alike");
+}
+
+// The host composition of attn_pack: +bias, RMS q/k, RoPE q/k from coords,
+// then pack_q / pack_kv (gpu/attention.mojo:507-662).
+struct HostPack {
+    std::vector<float> qh, kt, vh;
+};
+HostPack host_attn_pack(const std::vector<float>& qkv, const std::vector<float>& bias, const std::vector<float>& gq,
+                        const std::vector<float>& gk, const std::vector<int32_t>& coords, int64_t rows, int64_t h,
+                        int64_t d, int64_t mp, int64_t lp) {
+    const int64_t hd = h * d;
+    std::vector<float> t(qkv.size());
+    orc_add_bias(qkv.data(), bias.data(), t.data(), rows, 3 * hd);
+    std::vector<float> freqs((size_t)d / 2);
+    const int64_t fd = orc_rope_freqs(d, 3, 1.0, 10000.0, freqs.data());
+    std::vector<float> ph((size_t)(rows * d));
+    orc_rope_phases_from_coords(coords.data(), rows, 4, 3, d, freqs.data(), fd, ph.data());
+    for (int part = 0; part < 2; ++part) {
+        std::vector<float> a((size_t)(rows * hd)), r(a.size()), o(a.size());
+        for (int64_t i = 0; i < rows; ++i) std::memcpy(&a[(size_t)(i * hd)], &t[(size_t)(i * 3 * hd + part * hd)], (size_t)hd * 4);
+        orc_multihead_rmsnorm(a.data(), (part == 0 ? gq : gk).data(), r.data(), rows, h, d, 1);
+        orc_rope_rotate(r.data(), ph.data(), o.data(), rows, h, d, 1);
+        for (int64_t i = 0; i < rows; ++i) std::memcpy(&t[(size_t)(i * 3 * hd + part * hd)], &o[(size_t)(i * hd)], (size_t)hd * 4);
+    }
+    HostPack p{std::vector<float>((size_t)(h * mp * d)), std::vector<float>((size_t)(h * d * lp)),
+               std::vector<float>((size_t)(h * lp * d))};
+    orc_pack_q(t.data(), p.qh.data(), rows, h, d, mp, 3 * hd);
+    orc_pack_kv(t.data(), p.kt.data(), p.vh.data(), rows, h, d, lp);
+    p.qh = round_f16(p.qh);
+    p.kt = round_f16(p.kt);
+    p.vh = round_f16(p.vh);
+    return p;
+}
+
+void test_gpu_attn_pack() {
+    const int64_t rows = 70, h = 12, d = 128, hd = h * d, mp = 72, lp = 80, k = 256;
+    const auto bias = randn(91, 3 * hd, 0.02), gq = randn(92, hd, 0.02), gk = randn(93, hd, 0.02);
+    std::vector<float> gq1(gq), gk1(gk);
+    for (auto& v : gq1) v += 1.0f;
+    for (auto& v : gk1) v += 1.0f;
+    std::vector<int32_t> coords((size_t)rows * 4, 0);
+    orc_rng r;
+    orc_rng_init(&r, 94);
+    for (int64_t i = 0; i < rows; ++i)
+        for (int a = 1; a < 4; ++a) coords[(size_t)i * 4 + a] = (int32_t)(orc_rng_next_u64(&r) % 64);
+    const IntMatrix cm = IntMatrix::from_host(coords.data(), rows, 4);
+    gp::Rope rope;
+    rope.freqs = nn::rope_freqs(d);
+    rope.coords = &cm;
+    const Tensor bd = Tensor::from_host(bias.data(), {3 * hd}), gqd = Tensor::from_host(gq1.data(), {h, d}),
+                 gkd = Tensor::from_host(gk1.data(), {h, d});
+    auto compare = [&](const gp::AttnOperands& o, const HostPack& want, bool kt, const char* what) {
+        expect_close(o.qh.to_host(), want.qh, 2e-3, what);
+        expect_close(o.vh.to_host(), want.vh, 2e-3, what);
+        if (kt) {
+            expect_close(o.k.to_host(), want.kt, 2e-3, what);
+        } else {   // [H, lp, D] against the transposed [H, D, lp]
+            std::vector<float> krow(want.kt.size());
+            for (int64_t z = 0; z < h; ++z)
+                for (int64_t e = 0; e < d; ++e)
+                    for (int64_t t = 0; t < lp; ++t)
+                        krow[(size_t)((z * lp + t) * d + e)] = want.kt[(size_t)((z * d + e) * lp + t)];
+            expect_close(o.k.to_host(), krow, 2e-3, what);
+        }
+    };
+    // the epilogue + pack on a qkv GEMM output
+    const auto qkv = randn(95, rows * 3 * hd);
+    const Tensor qkvd = Tensor::from_host(qkv.data(), {rows, 3 * hd}, t2h::F16);
+    const HostPack want = host_attn_pack(round_f16(qkv), bias, gq1, gk1, coords, rows, h, d, mp, lp);
+    compare(gp::attn_pack(qkvd, (int32_t)h, bd, gqd, gkd, rope, mp, lp, true), want, true, "attn_pack, k transposed");
+    compare(gp::attn_pack(qkvd, (int32_t)h, bd, gqd, gkd, rope, mp, lp, false), want, false, "attn_pack, k row-major");
+    // the qkv GEMM with that epilogue and pack in its store
+    const auto x = round_f16(randn(96, rows * k, 0.5)), w = round_f16(randn(97, 3 * hd * k, 0.05));
+    const HostPack wl = host_attn_pack(host_linear(x, w, rows, 3 * hd, k), bias, gq1, gk1, coords, rows, h, d, mp, lp);
+    compare(gp::qkv_linear_pack(Tensor::from_host(x.data(), {rows, k}, t2h::F16),
+                                Tensor::from_host(w.data(), {3 * hd, k}, t2h::F16), (int32_t)h, bd, gqd, gkd, rope, mp,
+                                lp, true),
+            wl, true, "qkv_linear_pack");
+    expect_error([&] { gp::attn_pack(qkvd, 7, bd, gqd, gkd); }, "attn_pack: qkv must be [rows, 3 * H * D]");
+}
+
 // ---- samplers/flow_euler.mojo --------------------------------------------------------
 namespace smp = t2h::samplers;
 
@@ -631,6 +752,8 @@ int main(int argc, char** argv) {
         {"modulated_cross_block", test_modulated_cross_block},
         {"cross_block_enqueue", test_cross_block_enqueue},
         {"flow_euler_sampler", test_flow_euler_sampler},
+        {"gpu_linear", test_gpu_linear},
+        {"gpu_attn_pack", test_gpu_attn_pack},
         {"abi_errors_propagate", test_abi_errors_propagate},
     };
     if (argc > 1 && std::strcmp(argv[1], "--host") == 0) {   // the checks that need no GPU

@@ -56,4 +56,4 @@ def test_cpp_operator_interface(dev):
     p = _run([], 100)
     assert p.returncode == 0, p.stdout[-4000:]
     assert "FAIL" not in p.stdout
-    assert "17 of 17 passed" in p.stdout
+    assert "19 of 19 passed" in p.stdout
