@@ -49,6 +49,8 @@ def parse():
     p.add_argument("--configs-only", action="store_true",
                    help="time only BASELINE configs 1-4 and print their JSON (for profiler runs)")
     p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
+    p.add_argument("--sweep", action="store_true",
+                   help="time the config-5 chain at several token counts and print their JSON")
     p.add_argument("--probe", action="store_true",
                    help="time the HBM streaming probes (lib/libhbm_probe.so) instead of the chain")
     return p.parse_args()
@@ -59,14 +61,19 @@ class Chain:
 
     C, H, D, F = 1536, 12, 128, 6144
 
-    def __init__(self, dev, dtype):
+    def __init__(self, dev, dtype, tokens=None):
         import numpy as np
         import torch
 
         from t2h import nn, ops, workloads
 
         self.torch, self.ops, self.np = torch, ops, np
-        coords, offsets = workloads.config5()
+        if tokens is None:
+            coords, offsets = workloads.config5()
+        else:   # one batch of `tokens` voxels at random positions on the 128^3 grid
+            coords = np.zeros((tokens, 4), np.int32)
+            coords[:, 1:] = np.random.default_rng(tokens).integers(0, 128, (tokens, 3), dtype=np.int32)
+            offsets = np.array([0, tokens], np.int64)
         self.coords_np = coords
         self.T = T = coords.shape[0]
         C, H, D, F = self.C, self.H, self.D, self.F
@@ -666,6 +673,28 @@ def next_rows(torch, dev, chain, reps):
     return res
 
 
+def chain_sweep(torch, dev, steps):
+    """The config-5 chain (same ops, widths and f16 storage) at token counts
+    from the dense sparse-structure grid (4,096) to 2.6x config 5, one batch
+    of random voxels each: how the chain's HBM efficiency grows with T.
+    Prints one JSON line."""
+    res = {}
+    for tokens in (4096, 16384, 65536, 201436, 524288):
+        ch = Chain(dev, torch.float16, tokens)
+        for _ in range(3):
+            ch.step()
+        n = max(5, min(steps, int(2e5 // tokens) * 10))
+        ms = time_region(torch, ch.step, n) / n
+        gbs = ch.chain_bytes / ms / 1e6
+        res[str(tokens)] = {"us_per_step": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                            "pct_peak": round(gbs / HBM_PEAK_GBS * 100, 2), "tokens_per_s": round(tokens / ms * 1e3)}
+        log(f"  T={tokens:>7d}  {ms*1e3:9.1f} us/step  {gbs:8.1f} GB/s ({gbs/HBM_PEAK_GBS*100:5.1f}%)  "
+            f"{tokens/ms/1e3:8.1f} M tokens/s")
+        del ch
+        torch.cuda.empty_cache()
+    print(json.dumps({"chain_sweep": res, "bytes_per_token": 52240}), flush=True)
+
+
 def hbm_probes(torch, dev, steps):
     """The streaming probes of trellis2-mojo_amd/probe/hbm_probe.hip on the
     config-5 GELU tensor (f16 [201436, 6144]): what each access pattern and
@@ -712,6 +741,9 @@ def main():
     ops.device_init(0)
     if args.probe:
         hbm_probes(torch, dev, args.steps)
+        return
+    if args.sweep:
+        chain_sweep(torch, dev, args.steps)
         return
     if args.configs_only:
         log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
