@@ -198,3 +198,28 @@ def test_attn_pack_errors(dev):
         ops.attn_pack(x[:, 0], x[:, 1], gamma_q=torch.ones(h, 128, device=dev), use_rope=False)
     with pytest.raises(ValueError, match="needs phases, coords or grid_res"):
         ops.attn_pack(x[:, 0], freqs=nn.rope_freqs(128))
+
+
+@pytest.mark.parametrize("rows,h", [(2048, 4), (2369, 4), (2113, 4), (4096, 2), (4160, 16)])
+def test_reference_attention_shapes(dev, rows, h):
+    """The geometries of the reference's GPU attention parity test
+    (tests/parity/parity_wp11_gpu_attn.mojo:261-279: DiT self-attention,
+    the odd slat lengths 2369 and 2113, 2 heads at 4096 and 16 heads at 4160,
+    head_dim 64), through the epilogue + pack with a dense phase table, in f32
+    against the oracle, both k layouts."""
+    d = 64
+    qkv = orc.randn(2700 + rows + h, (rows, 3, h, d))
+    bias, gq, gk = _params(h, d, 2701)
+    pos = orc.Rng(2702 + rows).uniform((rows, 3), 0, 16).astype(np.float32)
+    phases = orc.rope_phases_from_positions(pos, d, orc.rope_freqs(d))
+    mp, lp = pad64(rows), pad64(rows)
+    wq, wk, wv = orc.attn_pack(qkv, h, d, mp, lp, bias.reshape(-1), gq, gk, phases)
+    q, k, v = _views(to_dev(qkv, dev), h, d)
+    b = to_dev(bias, dev)
+    for kt in (True, False):
+        qh, ko, vh = ops.attn_pack(q, k, v, mp=mp, lp=lp, bias_q=b[0], bias_k=b[1], bias_v=b[2],
+                                   gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(d),
+                                   phases=to_dev(phases, dev), k_transposed=kt)
+        assert_close(qh, wq, torch.float32, f"qh rows={rows} h={h}")
+        assert_close(ko if kt else ko.transpose(1, 2), wk, torch.float32, f"k transposed={kt} rows={rows} h={h}")
+        assert np.array_equal(host(vh), wv), "v: bias add and pack are exact"
