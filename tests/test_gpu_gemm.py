@@ -237,3 +237,80 @@ def test_one_two_three_k_steps_bit_exact(dev, k):
     args = dict(bias=to_dev(bias, dev), gate=to_dev(gate, dev), offsets=to_dev(offsets, dev))
     assert np.array_equal(host(ops.linear_gate_residual(ad, wd, to_dev(res, dev, torch.float16), **args)), want_r)
     assert np.array_equal(host(ops.linear_gate_residual(ad, wd, to_dev(res, dev), **args)), want_r)
+
+
+# ---- the reference GPU linear test's geometries ------------------------------
+# tests/parity/parity_wp11_gpu_linear.mojo:105-111: rows, out_features,
+# in_features, bias, and that test's absolute bar for the case.
+REF_SHAPES = [
+    (4096, 3072, 1024, True, 2e-4),
+    (1029, 1024, 1024, True, 2e-4),
+    (2369, 4096, 1024, True, 2e-4),
+    (2369, 1024, 4096, True, 4e-4),
+    (600, 6144, 1024, False, 2e-4),
+]
+
+
+def _ref_fill(seed, shape, scale):
+    """Operands distributed as the reference test's fill
+    (parity_wp11_gpu_linear.mojo:33-50): uniform in [-scale, scale)."""
+    return np.random.default_rng(seed).uniform(-scale, scale, shape).astype(np.float32)
+
+
+def _ref_case(seed, rows, co, ci, dtype, w_scale=0.03, b_scale=0.5):
+    """make_case (parity_wp11_gpu_linear.mojo:43-50) with x and w stored in
+    `dtype`, the way a 16-bit checkpoint and a 16-bit activation arrive."""
+    a = storage_round(_ref_fill(seed, (rows, ci), 1.0), dtype)
+    w = storage_round(_ref_fill(seed + 1, (co, ci), w_scale), dtype)
+    return a, w, _ref_fill(seed + 2, (co,), b_scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", range(len(REF_SHAPES)))
+def test_reference_linear_shapes(dev, dtype, case):
+    """DiT qkv / out / mlp / adaLN GEMMs at the reference test's shapes, odd
+    token counts (ragged last token tile) and k = 4096 among them: the f32
+    output is within the reference test's absolute bar of the oracle on the
+    same 16-bit operands, and within the summation-order bound."""
+    rows, co, ci, has_bias, atol = REF_SHAPES[case]
+    a, w, b = _ref_case(11 + case, rows, co, ci, dtype)
+    bias = b if has_bias else None
+    want = orc.linear(a, w, bias=bias)
+    got = host(ops.linear(to_dev(a, dev, dtype), to_dev(w, dev, dtype),
+                          bias=to_dev(b, dev) if has_bias else None, out_dtype=torch.float32))
+    err = np.abs(got - want)
+    assert err.max() <= atol, f"{rows}x{co}x{ci}: max |diff| {err.max():.3e} > {atol:g}"
+    assert np.all(err <= _sum_bound(a, w) + 2.0 ** -23 * np.abs(want))
+
+
+def test_reference_linear_3d_input(dev):
+    """A [1, 1500, 1024] dense-DiT activation to 3072 features
+    (parity_wp11_gpu_linear.mojo:113-126): output [1, 1500, 3072] within
+    2e-4 of the oracle."""
+    a, w, b = _ref_case(21, 1500, 3072, 1024, torch.float16)
+    got = ops.linear(to_dev(a, dev, torch.float16).reshape(1, 1500, 1024), to_dev(w, dev, torch.float16),
+                     bias=to_dev(b, dev), out_dtype=torch.float32)
+    assert got.shape == (1, 1500, 3072)
+    assert np.abs(host(got).reshape(1500, 3072) - orc.linear(a, w, bias=b)).max() <= 2e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_reference_mlp_chain(dev, dtype):
+    """The feed-forward chain lin2(gelu_tanh(lin0(x))) at 1500 x 1024 -> 4096
+    -> 1024 (parity_wp11_gpu_linear.mojo:166-194): the first GEMM's bias and
+    GELU in its store, the 4096-wide hidden stored in `dtype`, the second GEMM
+    with its bias; within the reference test's 5e-4 of the oracle's chain
+    (which rounds the hidden to `dtype` the same way)."""
+    rows, ci, hid = 1500, 1024, 4096
+    x = storage_round(_ref_fill(91, (rows, ci), 1.0), dtype)
+    w0 = storage_round(_ref_fill(92, (hid, ci), 0.03), dtype)
+    b0 = _ref_fill(93, (hid,), 0.1)
+    w2 = storage_round(_ref_fill(94, (ci, hid), 0.015), dtype)
+    b2 = _ref_fill(95, (ci,), 0.1)
+    mid = ops.linear(to_dev(x, dev, dtype), to_dev(w0, dev, dtype), bias=to_dev(b0, dev), act=ops.ACT_GELU_TANH)
+    assert mid.dtype == dtype
+    got = host(ops.linear(mid, to_dev(w2, dev, dtype), bias=to_dev(b2, dev), out_dtype=torch.float32))
+    want_mid = orc.linear(x, w0, bias=b0, act=ops.ACT_GELU_TANH)
+    assert_close(mid, storage_round(want_mid, dtype), dtype, "mlp hidden")
+    want = orc.linear(storage_round(want_mid, dtype), w2, bias=b2)
+    assert np.abs(got - want).max() <= 5e-4
