@@ -1,12 +1,14 @@
-"""INTEGRATION.md's Mojo bindings against the C ABI (no GPU, no Mojo): every
-`external_call["t2h_…", R](…)` names a function that include/t2h.h declares
-and passes as many arguments as the declaration takes, so the bindings a
-maintainer copies cannot drift from the library. The Mojo itself cannot be
-compiled here; this checks what can be checked from the text."""
+"""The integration guide's Mojo bindings against the C ABI (no GPU, no Mojo):
+every `external_call["t2h_…", R](…)` in the guide names a function that
+include/t2h.h declares and passes as many arguments as the declaration takes,
+so the bindings a maintainer copies cannot drift from the library. The Mojo
+itself cannot be compiled here; this checks what can be checked from the
+text."""
 import os
 import re
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = "INTEGRATION.md"
 
 
 def split_top(args: str):
@@ -38,7 +40,7 @@ def declared():
 
 
 def calls():
-    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    doc = open(os.path.join(ROOT, GUIDE)).read()
     found = []
     for m in re.finditer(r'external_call\["(t2h_\w+)",\s*[^\]]*\]?\]\(', doc):
         i, depth = m.end(), 1
@@ -55,6 +57,6 @@ def test_bindings_match_the_header():
     found = calls()
     assert len(found) >= 15
     for name, args in found:
-        assert name in decls, f"INTEGRATION.md calls {name}, which include/t2h.h does not declare"
+        assert name in decls, f"{GUIDE} calls {name}, which include/t2h.h does not declare"
         n = len(split_top(args))
-        assert n == decls[name], f"INTEGRATION.md passes {n} arguments to {name}; t2h.h declares {decls[name]}"
+        assert n == decls[name], f"{GUIDE} passes {n} arguments to {name}; t2h.h declares {decls[name]}"
