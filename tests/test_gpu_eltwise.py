@@ -38,6 +38,27 @@ def test_gelu_tanh_bias(dev, dtype, shape):
     assert_close(got, orc.gelu_tanh_bias(x, bias), dtype, f"GELU {dtype} {shape}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(9, 520), (3, 4104), (6, 512), (13, 264)])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_activation_slab_edges(dev, dtype, shape, with_bias):
+    """The one-vector-per-thread layout (1 KB column slabs of 4-row tiles) at
+    its edges: a last slab with a single live lane (520 f16 / bf16, 264 and
+    4104 f32), exactly one slab (512 f16), rows off the 4-row tile, and rows
+    narrower than a slab (264 f16), with and without the bias staged per
+    slab. The guard elements after the output stay untouched."""
+    rows, cols = shape
+    x = storage_round(orc.randn(330 + cols, shape, std=3.0), dtype)
+    bias = orc.randn(331 + cols, (cols,), std=0.02) if with_bias else None
+    buf = torch.full((rows * cols + 256,), 7.0, dtype=dtype, device=dev)
+    out = buf[: rows * cols].view(rows, cols)
+    ops.activation(to_dev(x, dev, dtype), ops.ACT_GELU_TANH, bias=to_dev(bias, dev) if with_bias else None,
+                   out=out)
+    want = orc.gelu_tanh_bias(x, bias) if with_bias else orc.activation(x, ops.ACT_GELU_TANH)
+    assert_close(out, want, dtype, f"GELU {dtype} {shape} bias={with_bias}")
+    assert bool((buf[rows * cols:] == 7).all())
+
+
 @pytest.mark.parametrize("kind", [ops.ACT_RELU, ops.ACT_SILU, ops.ACT_GELU, ops.ACT_GELU_TANH])
 def test_activation_kinds(dev, kind):
     x = orc.randn(320 + kind, (513, 1536), std=4.0)
@@ -86,6 +107,42 @@ def test_gate_residual_variants_bit_exact(dev, dtype):
     }
     for name, (got, want) in cases.items():
         assert bits_equal(got, want, dtype), f"{name} {dtype} not bit-exact"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(9, 520), (13, 264), (6, 4104), (11, 1536)])
+def test_gate_residual_tile_edges(dev, dtype, shape):
+    """The row-tiled gated residual at its edges: widths that are not a whole
+    number of 16-byte-vector blocks (520, 264, 4104), rows off the 4-row
+    tile, batch boundaries inside a tile (offsets 0, 3, 3, 6: an empty batch,
+    and rows 3-5 whose tile starts in batch 0) and rows_per_batch 5; with and
+    without bias, without x, in place over x. Bit-exact with the oracle; the
+    guard elements after the output stay untouched."""
+    rows, c = shape
+    x = storage_round(orc.randn(440 + c, shape), dtype)
+    h = storage_round(orc.randn(441 + c, shape), dtype)
+    gate = orc.randn(442 + c, (4, c), std=0.1)
+    bias = orc.randn(443 + c, (c,), std=0.05)
+    offsets = np.array([0, 3, 3, min(6, rows), rows], np.int64)
+    by5 = np.array(list(range(0, rows, 5)) + [rows], np.int64)
+    dx, dh, dg, db = to_dev(x, dev, dtype), to_dev(h, dev, dtype), to_dev(gate, dev), to_dev(bias, dev)
+    buf = torch.full((rows * c + 256,), 7.0, dtype=dtype, device=dev)
+    out = buf[: rows * c].view(rows, c)
+    cases = [
+        (dict(gate=dg, bias=db, offsets=to_dev(offsets, dev)), orc.gate_residual(x, h, gate, offsets, bias)),
+        (dict(gate=dg, offsets=to_dev(offsets, dev)), orc.gate_residual(x, h, gate, offsets)),
+        (dict(gate=dg, bias=db, rows_per_batch=5), orc.gate_residual(x, h, gate, by5, bias)),
+        (dict(bias=db), orc.gate_residual(x, h, None, None, bias)),
+    ]
+    for kw, want in cases:
+        buf.fill_(7.0)
+        ops.gate_residual(dx, dh, out=out, **kw)
+        assert bits_equal(out, want, dtype), f"{dtype} {shape} {sorted(kw)}"
+        assert bool((buf[rows * c:] == 7).all())
+    gated = orc.binop_rows(h, gate, orc.batch_broadcast_map(offsets), orc.OP_MUL)
+    assert bits_equal(ops.gate_residual(None, dh, gate=dg, offsets=to_dev(offsets, dev)), gated, dtype)
+    ops.gate_residual(dx, dh, gate=dg, bias=db, offsets=to_dev(offsets, dev), out=dx)   # in place
+    assert bits_equal(dx, orc.gate_residual(x, h, gate, offsets, bias), dtype)
 
 
 def test_dense_gate_api(dev):

@@ -122,6 +122,81 @@ __global__ __launch_bounds__(1024) void act_kernel(EltArgs a) {
     }
 }
 
+// Slab layout, one vector per thread: a wave covers 64 vectors (64 * V
+// columns, 1 KB) of one row, a block covers that column slab for kSlabRows
+// consecutive rows, and consecutive blocks walk the slabs of a row tile
+// (2-D grid: x = slab, y = row tile, dispatched x first; no index division).
+// Every thread moves exactly one 16-byte vector in and one out. The slab's
+// bias is read from global memory once per block (16 B for each thread of
+// the first V / 4 waves) into LDS, behind an LDS-only barrier that leaves the
+// row loads in flight. Measured on MI355X (config-5 GELU, f16
+// [201436, 6144]): one row per thread streams at ~84 % of HBM peak where the
+// several rows per thread that per-thread bias loads need to amortise stay
+// at ~76 %. Each wave lives for one load and one store, so its start-up
+// counts: the kernel takes a small argument block (one scalar load round)
+// and writes the bias to LDS in thread order (no bank conflicts on the
+// 16-byte stores).
+constexpr int kSlabRows = 4;
+constexpr int kSlabThreads = 64 * kSlabRows;
+
+struct SlabArgs {
+    const void* x;
+    void* out;
+    const float* bias;
+    int64_t rows;
+    int32_t cols;
+};
+
+__device__ __forceinline__ void lds_barrier() {
+    // lgkmcnt(0) covers this wave's LDS stores; the row loads (vmcnt) stay in
+    // flight across the barrier.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <typename T, int V, int KIND, bool BIAS>
+__global__ __launch_bounds__(kSlabThreads) void act_slab_kernel(SlabArgs a) {
+    constexpr int Q = V / 4;   // float4 pieces of a lane's bias
+    __shared__ float4 bl[BIAS ? 64 * Q : 1];   // the slab's bias in column order
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c0 = (int)blockIdx.x * (64 * V);   // < cols <= 2^31 - 1
+    const int64_t r = (int64_t)blockIdx.y * kSlabRows + wave;
+    const int col = c0 + lane * V;
+    const bool live = r < a.rows && col < a.cols;
+    float4 bq;
+    if (BIAS && wave < Q) {
+        // slab floats [4 * tid, 4 * tid + 4), clamped to the row (cols % 4 == 0)
+        const int f = 4 * tid < a.cols - c0 ? c0 + 4 * tid : a.cols - 4;
+        bq = *reinterpret_cast<const float4*>(a.bias + f);
+    }
+    // The row load is unconditional (indices clamped), so no lane's load sits
+    // behind a branch that would make the bias wait for it.
+    float v[V];
+    {
+        const int64_t rl = r < a.rows ? r : a.rows - 1;
+        const int cl = col < a.cols ? col : a.cols - V;
+        ld<T, V>(static_cast<const T*>(a.x) + rl * a.cols + cl, v);
+    }
+    float bias[V];
+    if constexpr (BIAS) {
+        if (wave < Q) bl[tid] = bq;
+        lds_barrier();
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const float4 w = bl[lane * Q + q];
+            bias[4 * q] = w.x; bias[4 * q + 1] = w.y; bias[4 * q + 2] = w.z; bias[4 * q + 3] = w.w;
+        }
+    }
+    if (!live) return;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = act_f<KIND>(BIAS ? bias_add(v[i], bias[i]) : v[i]);
+    st<T, V>(static_cast<T*>(a.out) + r * a.cols + col, v);
+}
+
 // ---- out = x + fl(fl(h + bias) * gate[b]) ------------------------------------
 template <typename T, int V>
 __global__ __launch_bounds__(1024) void gate_res_kernel(EltArgs a) {
@@ -159,6 +234,7 @@ __global__ __launch_bounds__(1024) void gate_res_kernel(EltArgs a) {
     }
     store_rows<T, V>(o, a.cols, t, hv);
 }
+
 
 // ---- out = fl(fl(x * fl(1 + scale[b])) + shift[b]) ---------------------------
 template <typename T, int V>
@@ -343,9 +419,22 @@ hipError_t tile_launch(K kernel, EltArgs a, hipStream_t s) {
         default: return FN<__bf16>(__VA_ARGS__);                       \
     }
 
+// The slab layout (act_slab_kernel) for 16-byte-aligned rows of at least one
+// slab; row-tiled kernels for the rest.
 template <typename T, int KIND, bool BIAS>
 hipError_t act_launch(const EltArgs& a, hipStream_t s) {
     constexpr int V = kPack<T>;
+    if (vec_ok<T>(a) && a.cols >= 64 * V) {
+        const int64_t slabs = (a.cols + 64 * V - 1) / (64 * V);
+        const int64_t tiles = (a.rows + kSlabRows - 1) / kSlabRows;
+        // a dispatch counts work-items in 32 bits per grid dimension
+        if (tiles < (int64_t(1) << 32) && slabs * kSlabThreads < (int64_t(1) << 32)) {
+            const SlabArgs sa{a.x, a.out, a.bias, a.rows, a.cols};
+            hipLaunchKernelGGL((act_slab_kernel<T, V, KIND, BIAS>), dim3((unsigned)slabs, (unsigned)tiles),
+                               dim3(kSlabThreads), 0, s, sa);
+            return hipGetLastError();
+        }
+    }
     if (vec_ok<T>(a)) return tile_launch<V>(act_kernel<T, V, KIND, BIAS>, a, s);
     return tile_launch<1>(act_kernel<T, 1, KIND, BIAS>, a, s);
 }
