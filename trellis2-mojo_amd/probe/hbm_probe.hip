@@ -108,7 +108,135 @@ int launch(const void* s, void* d, const float* bias, int64_t rows, hipStream_t 
     return (int)hipGetLastError();
 }
 
+// Head-major fan-out (the attention pack's write pattern): the [rows, 6144]
+// tensor is read as 4 slabs of 1536 columns (12 heads of 128 f16 = 256 B);
+// a block is 8 waves over 8 rows of one slab, one wave per row (3 x 1 KB
+// loads per wave). MODE 0 stores the rows back row-major (the contiguous
+// baseline); MODE 1 stores each head's 256 B straight into plane
+// [48 planes][rows][128], so one wave store covers 4 planes; MODE 2 stages
+// the 8 rows in LDS and stores 4 rows x 256 B of one plane per wave store,
+// 1 KB contiguous.
+// MODE 3 and 4 are MODE 0 and 1 with the waves of a block on 8 consecutive
+// (row, slab) pieces in memory order (2 whole rows, 24 KB contiguous)
+// instead of one slab of 8 rows (8 pieces 12 KB apart).
+template <int MODE>
+__global__ __launch_bounds__(512) void headmajor_probe(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                       int64_t rows) {
+    constexpr int kPitch = 1536 / 8 + 1;   // 16-byte vectors per LDS row (+1 against bank conflicts)
+    __shared__ u32x4 lds[MODE == 2 ? 8 * kPitch : 1];
+    const int64_t b = blockIdx.x;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t piece = b * 8 + wave;
+    const int slab = MODE >= 3 ? (int)(piece & 3) : (int)(b & 3);
+    const int64_t tile = b >> 2;
+    const int64_t r = MODE >= 3 ? piece >> 2 : tile * 8 + wave;
+    const int64_t rl = r < rows ? r : rows - 1;
+    u32x4 v[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) v[j] = __builtin_nontemporal_load(src + rl * kVpr + slab * 192 + j * 64 + lane);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) v[j].x ^= 0x3C003C00u;
+    if (MODE == 0 || MODE == 3) {
+        if (r < rows) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) __builtin_nontemporal_store(v[j], dst + r * kVpr + slab * 192 + j * 64 + lane);
+        }
+    } else if (MODE == 1 || MODE == 4) {
+        if (r < rows) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int plane = slab * 12 + j * 4 + (lane >> 4);
+                __builtin_nontemporal_store(v[j], dst + ((int64_t)plane * rows + r) * 16 + (lane & 15));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) lds[wave * kPitch + j * 64 + lane] = v[j];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int i = wave * 3 + j;          // 24 plane stores per block
+            const int h = i >> 1;                // head within the slab
+            const int rr = (i & 1) * 4 + (lane >> 4);
+            const int64_t row = tile * 8 + rr;
+            const u32x4 w = lds[rr * kPitch + h * 16 + (lane & 15)];
+            if (row < rows)
+                __builtin_nontemporal_store(w, dst + ((int64_t)(slab * 12 + h) * rows + row) * 16 + (lane & 15));
+        }
+    }
+}
+
+template <int MODE>
+int launch_hm(const void* s, void* d, const float*, int64_t rows, hipStream_t st) {
+    const int64_t nb = (rows + 7) / 8 * 4;
+    hipLaunchKernelGGL((headmajor_probe<MODE>), dim3((unsigned)nb), dim3(512), 0, st, static_cast<const u32x4*>(s),
+                       static_cast<u32x4*>(d), rows);
+    return (int)hipGetLastError();
+}
+
 typedef int (*Launch)(const void*, void*, const float*, int64_t, hipStream_t);
+// One 16-byte vector per thread (one row per thread), with the bias shared
+// by the rows of a block through LDS: a block is RPB rows x WPR waves per
+// row, covering a column slab of WPR * 512 elements (1 KB per wave, 12 / WPR
+// slabs per row, slab-fastest block order dealt to P fronts). KIND 1 loads
+// the slab's f32 bias once per block (16 B per thread of the first
+// WPR * 128) into LDS behind an LDS-only barrier that leaves the row load in
+// flight; every thread then reads its 32 B of bias from LDS.
+// P = 0: a 2-D grid (x = slab, y = row tile) instead of the 1-D block index.
+template <int WPR, int RPB, int KIND, int P>
+__global__ __launch_bounds__(WPR * RPB * 64) void slab_probe(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                            const float* __restrict__ bias, int64_t rows,
+                                                            int64_t nb, int64_t per) {
+    static_assert(RPB >= 2 && 12 % WPR == 0, "shape");
+    constexpr int S = 12 / WPR;       // column slabs per row
+    constexpr int SV = WPR * 64;      // 16-byte vectors per slab row
+    __shared__ float4 bl[KIND == 1 ? 2 * SV : 1];
+    const int64_t b = P == 0 ? (int64_t)blockIdx.y * S + blockIdx.x
+                             : (int64_t)(blockIdx.x % P) * per + blockIdx.x / P;
+    if (b >= nb) return;   // block-uniform, before the barrier
+    const int slab = P == 0 ? (int)blockIdx.x : (int)(b % S);
+    const int64_t tile = P == 0 ? (int64_t)blockIdx.y : b / S;
+    const int wave = threadIdx.x >> 6;
+    const int j = (wave % WPR) * 64 + (threadIdx.x & 63);   // vector within the slab row
+    const int64_t r = tile * RPB + wave / WPR;
+    const int c = slab * SV + j;
+    float4 bq = {0.f, 0.f, 0.f, 0.f};
+    if (KIND == 1 && threadIdx.x < 2 * SV) bq = reinterpret_cast<const float4*>(bias)[slab * 2 * SV + threadIdx.x];
+    const int64_t rl = r < rows ? r : rows - 1;
+    u32x4 v = __builtin_nontemporal_load(src + rl * kVpr + c);
+    if (KIND == 1) {
+        if (threadIdx.x < 2 * SV) bl[threadIdx.x] = bq;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS stores are done
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const float4 a0 = bl[2 * j], a1 = bl[2 * j + 1];
+        const float bv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        v = gelu8<true>(v, bv);
+    } else {
+        v.x ^= 0x3C003C00u;
+    }
+    if (r < rows) __builtin_nontemporal_store(v, dst + r * kVpr + c);
+}
+
+template <int WPR, int RPB, int KIND, int P>
+int launch_slab(const void* s, void* d, const float* bias, int64_t rows, hipStream_t st) {
+    const int64_t nb = (rows + RPB - 1) / RPB * (12 / WPR);
+    const int64_t per = P == 0 ? nb : (nb + P - 1) / P;
+    const dim3 grid = P == 0 ? dim3(12 / WPR, (unsigned)((rows + RPB - 1) / RPB)) : dim3((unsigned)(per * P));
+    hipLaunchKernelGGL((slab_probe<WPR, RPB, KIND, P>), grid, dim3(WPR * RPB * 64), 0, st,
+                       static_cast<const u32x4*>(s), static_cast<u32x4*>(d), bias, rows, nb, per);
+    return (int)hipGetLastError();
+}
+
+// The same probe writing its output over its input (each thread stores
+// exactly the vectors it loaded).
+template <Launch F>
+int in_place(const void* s, void*, const float* bias, int64_t rows, hipStream_t st) {
+    return F(s, const_cast<void*>(s), bias, rows, st);
+}
+
 struct Probe {
     const char* name;
     Launch fn;
@@ -125,6 +253,26 @@ const Probe kProbes[] = {
     {"copy W128 rpt6 P1", launch<128, 6, 0, 1>}, {"copy rpt4 P1 serial", launch<768, 4, 0, 1, 1>},
     {"copy rpt4 P1 strided", launch<768, 4, 0, 1, 0, 1>},
     {"gelu+bias W384 rpt2 P1", launch<384, 2, 1, 1>}, {"gelu+bias W256 rpt3 P1", launch<256, 3, 1, 1>},
+    // the attention pack's head-major fan-out
+    {"slab copy row-major", launch_hm<0>}, {"slab copy head-major direct", launch_hm<1>},
+    {"slab copy head-major via LDS", launch_hm<2>},
+    // in place: the stores go to the lines the loads just read
+    {"copy W256 rpt1 P1 in place", in_place<launch<256, 1, 0, 1>>},
+    {"copy rpt4 P1 in place", in_place<launch<768, 4, 0, 1>>},
+    {"gelu+bias rpt4 P1 in place", in_place<launch<768, 4, 1, 1>>},
+    {"slab copy row-major in place", in_place<launch_hm<0>>},
+    {"piece-order copy row-major", launch_hm<3>}, {"piece-order copy head-major direct", launch_hm<4>},
+    // one row per thread, rows of a block sharing the bias through LDS
+    {"slab copy 1x8", launch_slab<1, 8, 0, 1>},   {"slab copy 1x4", launch_slab<1, 4, 0, 1>},
+    {"slab copy 2x4", launch_slab<2, 4, 0, 1>},   {"slab copy 4x4", launch_slab<4, 4, 0, 1>},
+    {"slab copy 4x2", launch_slab<4, 2, 0, 1>},   {"slab copy 1x16", launch_slab<1, 16, 0, 1>},
+    {"slab copy 1x8 P8", launch_slab<1, 8, 0, 8>}, {"slab copy 4x4 P8", launch_slab<4, 4, 0, 8>},
+    {"slab gelu+bias 1x8", launch_slab<1, 8, 1, 1>},   {"slab gelu+bias 1x4", launch_slab<1, 4, 1, 1>},
+    {"slab gelu+bias 2x4", launch_slab<2, 4, 1, 1>},   {"slab gelu+bias 4x4", launch_slab<4, 4, 1, 1>},
+    {"slab gelu+bias 4x2", launch_slab<4, 2, 1, 1>},   {"slab gelu+bias 1x16", launch_slab<1, 16, 1, 1>},
+    {"slab gelu+bias 1x8 P8", launch_slab<1, 8, 1, 8>}, {"slab gelu+bias 4x4 P8", launch_slab<4, 4, 1, 8>},
+    {"slab gelu+bias 1x4 2-D grid", launch_slab<1, 4, 1, 0>}, {"slab gelu+bias 1x2", launch_slab<1, 2, 1, 1>},
+    {"slab copy 1x4 2-D grid", launch_slab<1, 4, 0, 0>},
 };
 
 }  // namespace
