@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as orc
-from _parity import assert_close, host, max_err, storage_round, to_dev
+from _parity import assert_close, bits_equal, host, max_err, storage_round, to_dev
 from t2h import nn, ops, sparse, workloads
 
 pytestmark = pytest.mark.gpu
@@ -196,3 +196,53 @@ def test_qk_errors(dev):
         nn.RotaryPositionEmbedder(127)
     with pytest.raises(ValueError):  # RoPE without a position source
         ops.qk_rmsnorm_rope(q=torch.zeros((4, 12, 128), device=dev), freqs=orc.rope_freqs(128))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("h", [4, 6, 8, 12, 16])
+@pytest.mark.parametrize("source", ["coords", "grid", "table"])
+def test_16bit_head_groups_and_sources(dev, dtype, h, source):
+    """16-bit rows with head_dim 128 (config 5's storage): 1-4 groups of 4
+    heads per wave instruction, one with an idle tail (6 heads), 301 rows (a
+    partial last tile), the three position sources (int coords, the dense
+    grid index, a phase table), q and k biases, against the oracle; then q
+    alone in place, and the packed qkv with its v bias (bit-exact after one
+    rounding)."""
+    rows, d = 301, 128
+    q = storage_round(orc.randn(1000 + h, (rows, h, d)), dtype)
+    k = storage_round(orc.randn(1001 + h, (rows, h, d)), dtype)
+    gq, gk = _gammas(h, d, 1002 + h)
+    bq, bk = orc.randn(1004 + h, (h, d), std=0.1), orc.randn(1005 + h, (h, d), std=0.1)
+    freqs = orc.rope_freqs(d)
+    coords = np.zeros((rows, 4), np.int32)
+    coords[:, 1:] = np.random.default_rng(h).integers(0, 128, (rows, 3))
+    src = {}
+    if source == "coords":
+        phases = orc.rope_phases_from_coords(coords, d, freqs)
+        src = dict(coords=to_dev(coords, dev))
+    elif source == "grid":
+        phases = orc.rope_phases_from_positions(np.tile(orc.grid_positions(8), (2, 1))[:rows], d, freqs)
+        src = dict(grid_res=8)
+    else:
+        phases = orc.rope_phases_from_positions(orc.randn(1006, (rows, 3), std=40.0), d, freqs)
+        src = dict(phases=to_dev(phases, dev))
+    wq, wk = orc.qk_rms_rope(q, k, gq, gk, phases, bias_q=bq, bias_k=bk)
+    dq, dk = to_dev(q, dev, dtype), to_dev(k, dev, dtype)
+    qo, ko = ops.qk_rmsnorm_rope(q=dq, k=dk, gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev),
+                                 bias_q=to_dev(bq, dev), bias_k=to_dev(bk, dev), freqs=freqs, **src)
+    assert_close(qo, wq, dtype, f"q {dtype} H={h} {source}")
+    assert_close(ko, wk, dtype, f"k {dtype} H={h} {source}")
+    ops.qk_rmsnorm_rope(q=dq, gamma_q=to_dev(gq, dev), freqs=freqs, in_place=True, **src)
+    wq1, _ = orc.qk_rms_rope(q, k, gq, gk, phases)
+    assert_close(dq, wq1, dtype, f"q in place {dtype} H={h} {source}")
+    qkv = storage_round(orc.randn(1007 + h, (rows, 3, h, d)), dtype)
+    bias = orc.randn(1008 + h, (3 * h * d,), std=0.1)
+    b3 = bias.reshape(3, h, d)
+    dqkv = to_dev(qkv.reshape(rows, -1), dev, dtype)
+    ops.qkv_bias_rmsnorm_rope(dqkv, h, d, bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev),
+                              freqs=freqs, **src)
+    got = dqkv.reshape(rows, 3, h, d)
+    pq, pk = orc.qk_rms_rope(qkv[:, 0], qkv[:, 1], gq, gk, phases, bias_q=b3[0], bias_k=b3[1])
+    assert_close(got[:, 0], pq, dtype, "packed q")
+    assert_close(got[:, 1], pk, dtype, "packed k")
+    assert bits_equal(got[:, 2].contiguous(), (qkv[:, 2] + b3[2]).astype(np.float32), dtype), "v bias"
