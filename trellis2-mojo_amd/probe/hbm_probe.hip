@@ -230,6 +230,64 @@ int launch_slab(const void* s, void* d, const float* bias, int64_t rows, hipStre
     return (int)hipGetLastError();
 }
 
+// Rows of 1536 f16 (3 KB, the width of LN / QK / the gated residual): the
+// [rows, 6144] buffers read as [4 * rows, 1536], 192 vectors per row.
+//   MODE 0  one wave per row, 3 vectors per lane, 8 rows per block (LN / QK shape)
+//   MODE 1  3 waves per row, one vector per lane, 4 rows per block (12 waves)
+//   MODE 2  4 waves on 4 rows of one 1 KB piece; consecutive blocks walk the 3 pieces
+//   MODE 3  3 waves per row, one vector per lane, 2 rows per block (6 waves)
+//   MODE 4  one wave per row, 3 vectors per lane, 4 rows per block
+constexpr int kNarrowVpr = 192;
+template <int MODE>
+constexpr int narrow_waves() { return MODE == 0 ? 8 : MODE == 1 ? 12 : MODE == 3 ? 6 : 4; }
+template <int MODE>
+constexpr int narrow_rows() { return MODE == 0 ? 8 : MODE == 3 ? 2 : 4; }
+
+template <int MODE>
+__global__ __launch_bounds__(narrow_waves<MODE>() * 64) void narrow_probe(const u32x4* __restrict__ src,
+                                                                           u32x4* __restrict__ dst, int64_t rows) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t b = blockIdx.x;
+    if (MODE == 0 || MODE == 4) {
+        const int64_t r = b * narrow_rows<MODE>() + wave;
+        const int64_t rl = r < rows ? r : rows - 1;
+        u32x4 v[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) v[j] = __builtin_nontemporal_load(src + rl * kNarrowVpr + j * 64 + lane);
+        if (r < rows) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                v[j].x ^= 0x3C003C00u;
+                __builtin_nontemporal_store(v[j], dst + r * kNarrowVpr + j * 64 + lane);
+            }
+        }
+    } else {
+        int64_t r;
+        int piece;
+        if (MODE == 2) {
+            piece = (int)(b % 3);
+            r = b / 3 * 4 + wave;
+        } else {
+            piece = wave % 3;
+            r = b * narrow_rows<MODE>() + wave / 3;
+        }
+        const int64_t rl = r < rows ? r : rows - 1;
+        u32x4 v = __builtin_nontemporal_load(src + rl * kNarrowVpr + piece * 64 + lane);
+        v.x ^= 0x3C003C00u;
+        if (r < rows) __builtin_nontemporal_store(v, dst + r * kNarrowVpr + piece * 64 + lane);
+    }
+}
+
+template <int MODE>
+int launch_narrow(const void* s, void* d, const float*, int64_t rows, hipStream_t st) {
+    const int64_t nrows = rows * 4;   // [rows, 6144] as [4 * rows, 1536]
+    const int64_t nb = MODE == 2 ? (nrows + 3) / 4 * 3 : (nrows + narrow_rows<MODE>() - 1) / narrow_rows<MODE>();
+    hipLaunchKernelGGL((narrow_probe<MODE>), dim3((unsigned)nb), dim3(narrow_waves<MODE>() * 64), 0, st,
+                       static_cast<const u32x4*>(s), static_cast<u32x4*>(d), nrows);
+    return (int)hipGetLastError();
+}
+
 // The same probe writing its output over its input (each thread stores
 // exactly the vectors it loaded).
 template <Launch F>
@@ -273,6 +331,10 @@ const Probe kProbes[] = {
     {"slab gelu+bias 1x8 P8", launch_slab<1, 8, 1, 8>}, {"slab gelu+bias 4x4 P8", launch_slab<4, 4, 1, 8>},
     {"slab gelu+bias 1x4 2-D grid", launch_slab<1, 4, 1, 0>}, {"slab gelu+bias 1x2", launch_slab<1, 2, 1, 1>},
     {"slab copy 1x4 2-D grid", launch_slab<1, 4, 0, 0>},
+    // 3 KB rows (1536 f16)
+    {"narrow copy wave per row x8", launch_narrow<0>}, {"narrow copy wave per row x4", launch_narrow<4>},
+    {"narrow copy 3 waves per row x4", launch_narrow<1>}, {"narrow copy 3 waves per row x2", launch_narrow<3>},
+    {"narrow copy 1 KB piece x4 rows", launch_narrow<2>},
 };
 
 }  // namespace
