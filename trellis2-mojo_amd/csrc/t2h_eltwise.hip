@@ -424,7 +424,8 @@ hipError_t tile_launch(K kernel, EltArgs a, hipStream_t s) {
 template <typename T, int KIND, bool BIAS>
 hipError_t act_launch(const EltArgs& a, hipStream_t s) {
     constexpr int V = kPack<T>;
-    if (vec_ok<T>(a) && a.cols >= 64 * V) {
+    // column indices stay in int32: the last slab's lanes reach cols - 1 + 64 * V
+    if (vec_ok<T>(a) && a.cols >= 64 * V && a.cols <= INT32_MAX - 64 * V) {
         const int64_t slabs = (a.cols + 64 * V - 1) / (64 * V);
         const int64_t tiles = (a.rows + kSlabRows - 1) / kSlabRows;
         // a dispatch counts work-items in 32 bits per grid dimension
