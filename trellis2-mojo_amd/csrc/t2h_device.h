@@ -243,6 +243,15 @@ struct BatchMap {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
+// Block barrier that waits only for LDS: lgkmcnt(0) covers this wave's LDS
+// stores, and the wave's global loads (vmcnt) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Linear block index of a launch on grid_1d()'s grid (a second grid
 // dimension only past 2^20 blocks; see t2h_internal.h).
 __device__ __forceinline__ int64_t block_linear() { return (int64_t)blockIdx.y * gridDim.x + blockIdx.x; }

@@ -147,15 +147,6 @@ struct SlabArgs {
     int32_t cols;
 };
 
-__device__ __forceinline__ void lds_barrier() {
-    // lgkmcnt(0) covers this wave's LDS stores; the row loads (vmcnt) stay in
-    // flight across the barrier.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 template <typename T, int V, int KIND, bool BIAS>
 __global__ __launch_bounds__(kSlabThreads) void act_slab_kernel(SlabArgs a) {
     constexpr int Q = V / 4;   // float4 pieces of a lane's bias

@@ -363,6 +363,94 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     }
 }
 
+// The v pass in the slab layout of the activation kernel: one 16-byte vector
+// per thread. A wave covers 1 KB of one row's v (64 * V columns, i.e. 4
+// heads of 128 f16), a block that piece for kVSlabRows consecutive rows, and
+// consecutive blocks walk the pieces of a row tile (2-D grid: x = piece, y =
+// row tile over lp). The piece's bias_v is read once per block into LDS
+// behind an LDS-only barrier that leaves the row loads in flight. A vector
+// lies inside one head (head_dim % V == 0) and lands at vh[h][r][d]; pad rows
+// rows <= r < lp are zero. One vector per thread streams faster than the row
+// wave's three (MI355X, 3 KB row pieces: ~81 % against ~71 % of HBM peak in
+// the streaming probes).
+constexpr int kVSlabRows = 4;
+constexpr int kVSlabThreads = 64 * kVSlabRows;
+
+struct PackVArgs {
+    const void* v;      // [rows, H * D], rows in_stride apart
+    void* vh;           // [H, lp, D]
+    const float* bias;  // [H * D] or nullptr
+    int64_t rows;
+    int64_t lp;
+    int64_t in_stride;
+    int32_t cols;       // H * D
+    int32_t dshift;     // log2(head_dim)
+};
+
+template <typename T, int V>
+__global__ __launch_bounds__(kVSlabThreads) void pack_v_slab_kernel(PackVArgs a) {
+    constexpr int Q = V / 4;   // float4 pieces of a lane's bias
+    __shared__ float4 bl[64 * Q];   // the piece's bias in column order
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c0 = (int)blockIdx.x * (64 * V);   // < cols
+    const int64_t r = (int64_t)blockIdx.y * kVSlabRows + wave;
+    const int col = c0 + lane * V;
+    const bool in_row = col < a.cols;
+    const bool live = r < a.rows;
+    const bool bias = a.bias != nullptr;   // block-uniform
+    float4 bq;
+    if (bias && wave < Q) {
+        const int f = 4 * tid < a.cols - c0 ? c0 + 4 * tid : a.cols - 4;   // cols % 4 == 0
+        bq = *reinterpret_cast<const float4*>(a.bias + f);
+    }
+    float v[V];
+    if (a.rows > 0) {   // unconditional (clamped) row load; no rows at all: pads only
+        const int64_t rl = live ? r : a.rows - 1;
+        const int cl = in_row ? col : a.cols - V;
+        load_elems<T, V, true>(static_cast<const T*>(a.v) + rl * a.in_stride + cl, v);
+    }
+    float b[V];
+    if (bias) {
+        if (wave < Q) bl[tid] = bq;
+        lds_barrier();
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const float4 w = bl[lane * Q + q];
+            b[4 * q] = w.x; b[4 * q + 1] = w.y; b[4 * q + 2] = w.z; b[4 * q + 3] = w.w;
+        }
+    }
+    if (r >= a.lp || !in_row) return;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = !live ? 0.0f : bias ? add_rn(v[i], b[i]) : v[i];
+    const int h = col >> a.dshift;
+    const int d = col - (h << a.dshift);
+    store_elems<T, V, true>(static_cast<T*>(a.vh) + (((int64_t)h * a.lp + r) << a.dshift) + d, v);
+}
+
+// The v pass goes to pack_v_slab_kernel when its rows are 16-byte vectors
+// of at least one slab; returns false when the row kernels must take it.
+template <typename T>
+bool v_slab_ok(const PackArgs& a) {
+    constexpr int V = kPack<T>;
+    const int64_t cols = (int64_t)a.heads * a.head_dim;
+    return a.vh != nullptr && cols >= 64 * V && cols <= INT32_MAX - 64 * V && a.in_stride % V == 0 &&
+           reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && (a.lp + kVSlabRows - 1) / kVSlabRows < (int64_t(1) << 32);
+}
+
+template <typename T>
+hipError_t launch_v_slab(const PackArgs& a, hipStream_t s) {
+    constexpr int V = kPack<T>;
+    const int32_t cols = a.heads * a.head_dim;
+    const PackVArgs va{a.v, a.vh, a.bias_v, a.rows, a.lp, a.in_stride, cols, a.head_dim == 128 ? 7 : 6};
+    const int64_t pieces = (cols + 64 * V - 1) / (64 * V);
+    const int64_t tiles = (a.lp + kVSlabRows - 1) / kVSlabRows;
+    hipLaunchKernelGGL((pack_v_slab_kernel<T, V>), dim3((unsigned)pieces, (unsigned)tiles), dim3(kVSlabThreads), 0, s,
+                       va);
+    return hipGetLastError();
+}
+
 // Heads per block: all of them when the row tiles alone fill the GPU,
 // else the largest divisor of heads that still gives ~8 blocks per CU.
 int heads_per_block(int64_t tiles, int tensors, int heads) {
@@ -380,9 +468,13 @@ hipError_t launch_d(const PackArgs& a, const RopeSlots& tab, hipStream_t s) {
     const int64_t ext = a.mp > a.lp ? a.mp : a.lp;
     const int64_t tiles = (ext + kPackRows - 1) / kPackRows;
     PackOrder rows{};
+    const bool v_slab = v_slab_ok<T>(a);
     if (a.qh != nullptr) rows.which[rows.n++] = 0;
     if (a.k_out != nullptr && !a.k_transposed) rows.which[rows.n++] = 1;
-    if (a.vh != nullptr) rows.which[rows.n++] = 2;
+    if (a.vh != nullptr && !v_slab) rows.which[rows.n++] = 2;
+    if (v_slab) {
+        if (hipError_t e = launch_v_slab<T>(a, s); e != hipSuccess) return e;
+    }
     if (rows.n > 0 && a.heads <= 16) {
         const int64_t blocks = (ext + kRowWaves - 1) / kRowWaves * rows.n;
         switch ((a.heads + 3) / 4) {
