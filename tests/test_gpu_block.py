@@ -155,3 +155,37 @@ def test_sparse_cross_block_config4(dev, dtype):
     rnd = lambda a: storage_round(a, dtype)
     want = orc.cross_block(rnd(x), chunks, w2, b2, *orc_chains(), offsets=offsets, store=rnd)
     assert_close(got.feats, want, dtype, f"sparse block {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("form", ["resident", "dense", "sparse"])
+def test_reference_block_geometry(dev, dtype, form):
+    """The per-token glue at the geometry of the reference's whole-block GPU
+    parity cases (tests/parity/parity_wp11_gpu_attn.mojo:495-536: width
+    1024, a dense block of L = 2048 and a sparse block of T = 2369 tokens):
+    the resident form over the const buffer, the dense [1, L, C] block and
+    the sparse feats, against the oracle."""
+    c = 1024
+    rows = 2369 if form == "sparse" else 2048
+    x = orc.randn(1600 + rows, (rows, c))
+    rnd = lambda a: storage_round(a, dtype)
+    m, w2, b2, biases = block_params(1601, c)
+    if form == "resident":
+        bk = block.pack_block_consts([to_dev(mm, dev) for mm in m], to_dev(w2, dev), to_dev(b2, dev),
+                                     *[to_dev(b, dev) for b in biases])
+        got = block.cross_block_enqueue(to_dev(x, dev, dtype), bk, *dev_chains(), fused=True)
+        want = orc.cross_block_resident(rnd(x), host(bk), *orc_chains(), store=rnd)
+        assert_close(got, want, dtype, f"resident block C=1024 {dtype}")
+        return
+    mod = np.concatenate(m, axis=1)   # [1, 6C]: the six chunks in adaLN order
+    blk = block.ModulatedCrossBlock(c, to_dev(w2, dev), to_dev(b2, dev))
+    if form == "dense":
+        got = blk(to_dev(x, dev, dtype).reshape(1, rows, c), to_dev(mod, dev),
+                  lambda h: dev_chains()[0](h.reshape(rows, c)), *dev_chains()[1:]).reshape(rows, c)
+    else:
+        coords = np.zeros((rows, 4), np.int32)
+        coords[:, 1:] = np.stack([np.arange(rows) // 256, (np.arange(rows) // 16) % 16, np.arange(rows) % 16], 1)
+        st = sparse.SparseTensor(to_dev(x, dev, dtype), to_dev(coords, dev), 1)
+        got = blk(st, to_dev(mod, dev), *dev_chains()).feats
+    want = orc.cross_block(rnd(x), m, w2, b2, *orc_chains(), offsets=np.array([0, rows], np.int64), store=rnd)
+    assert_close(got, want, dtype, f"{form} block C=1024 {dtype}")

@@ -246,3 +246,30 @@ def test_16bit_head_groups_and_sources(dev, dtype, h, source):
     assert_close(got[:, 0], pq, dtype, "packed q")
     assert_close(got[:, 1], pk, dtype, "packed k")
     assert bits_equal(got[:, 2].contiguous(), (qkv[:, 2] + b3[2]).astype(np.float32), dtype), "v bias"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows", [2048, 2369])
+def test_reference_block_geometry(dev, dtype, rows):
+    """QK RMSNorm + RoPE at the attention geometry of the reference's
+    whole-block GPU cases (tests/parity/parity_wp11_gpu_attn.mojo:495-536:
+    width 1024 as 16 heads of 64, L = 2048 dense on the 16^3 grid's first
+    rows, T = 2369 sparse from coords) against the oracle."""
+    h, d = 16, 64
+    q = storage_round(orc.randn(1100 + rows, (rows, h, d)), dtype)
+    k = storage_round(orc.randn(1101 + rows, (rows, h, d)), dtype)
+    gq, gk = _gammas(h, d, 1102)
+    freqs = orc.rope_freqs(d)
+    if rows == 2048:
+        phases = orc.rope_phases_from_positions(orc.grid_positions(16)[:rows], d, freqs)
+        src = dict(grid_res=16)
+    else:
+        coords = np.zeros((rows, 4), np.int32)
+        coords[:, 1:] = np.random.default_rng(rows).integers(0, 64, (rows, 3))
+        phases = orc.rope_phases_from_coords(coords, d, freqs)
+        src = dict(coords=to_dev(coords, dev))
+    wq, wk = orc.qk_rms_rope(q, k, gq, gk, phases)
+    qo, ko = ops.qk_rmsnorm_rope(q=to_dev(q, dev, dtype), k=to_dev(k, dev, dtype), gamma_q=to_dev(gq, dev),
+                                 gamma_k=to_dev(gk, dev), freqs=freqs, **src)
+    assert_close(qo, wq, dtype, f"q {dtype} rows={rows}")
+    assert_close(ko, wk, dtype, f"k {dtype} rows={rows}")
