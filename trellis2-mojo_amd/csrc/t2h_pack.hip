@@ -247,7 +247,9 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     constexpr int P = L::P;
     constexpr int VE = L::VE;
     constexpr int HALF = D / 2;
-    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];
+    constexpr int KP = (NG * 4 * D + kRowBlock - 1) / kRowBlock;   // parameter values per thread
+    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];   // gamma * scale
+    __shared__ __attribute__((aligned(16))) float bs[NG * 4 * D];   // bias
     const int lane = lane_id();
     const int g = lane >> 4;
     const int m = lane & 15;
@@ -273,6 +275,16 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     float cpos = 0.0f;
     if (live && coord_pos && my_axis >= 0) cpos = (float)a.coords[r * a.coord_cols + 1 + my_axis];
 
+    // The tensor's gamma and bias rows, staged in LDS once per block; their
+    // loads go out before the row loads so the staging waits for them alone.
+    const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
+    float gl[KP], bl[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        const int i = threadIdx.x + k * kRowBlock;
+        if (gamma != nullptr && i < H * D) gl[k] = gamma[i];
+        if (bias != nullptr && i < H * D) bl[k] = bias[i];
+    }
     const int64_t rl = live ? r : (a.rows > 0 ? a.rows - 1 : 0);
     float v[NG][E];
     if (a.rows > 0) {
@@ -288,8 +300,11 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
 #pragma unroll
             for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
     }
-    if (gamma != nullptr) {
-        for (int i = threadIdx.x; i < H * D; i += kRowBlock) gs[i] = gamma[i] * a.rms_scale;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        const int i = threadIdx.x + k * kRowBlock;
+        if (gamma != nullptr && i < H * D) gs[i] = gl[k] * a.rms_scale;
+        if (bias != nullptr && i < H * D) bs[i] = bl[k];
     }
     float pc[P], ps[P];
     if (rope) {
@@ -311,12 +326,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
             }
         }
     }
-    if (gamma != nullptr) {
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS stores are done
-        __builtin_amdgcn_s_barrier();
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
+    if (stage) lds_barrier();
     if (r >= extent) return;
 
 #pragma unroll
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
         float* x = v[it];
         if (bias != nullptr) {
             float bv[E];
-            L::params(bias + (int64_t)hh * D, m, bv);
+            L::params(&bs[hh * D], m, bv);
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = add_rn(x[i], bv[i]);
         }

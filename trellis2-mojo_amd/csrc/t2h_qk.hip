@@ -17,9 +17,9 @@
 //
 // Order inside a wave: slot-coordinate load, then the row loads (all
 // unconditional, so they are in flight together), then the block stages the
-// tensor's gamma * scale into LDS and meets at an LDS-only barrier
-// (lgkmcnt(0) + s_barrier, no vmcnt wait: the row loads stay in flight across
-// it). The grid is not persistent: many short blocks stream HBM better on
+// tensor's gamma * scale and bias into LDS (no lane reloads a per-head
+// parameter from L2) and meets at an LDS-only barrier (lgkmcnt(0) +
+// s_barrier). The grid is not persistent: many short blocks stream HBM better on
 // MI355X than waves that loop over rows.
 //
 // Reference: sparse/attention/modules.mojo:37-102 (MultiHeadRMSNorm),
@@ -48,7 +48,8 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     constexpr int P = L::P;
     constexpr int VE = L::VE;
     constexpr int HALF = D / 2;
-    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];
+    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];   // gamma * scale
+    __shared__ __attribute__((aligned(16))) float bs[NG * 4 * D];   // bias (q, k or v)
     const int lane = lane_id();
     const int g = lane >> 4;
     const int m = lane & 15;
@@ -67,22 +68,26 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     const int64_t r = tile * W + wave;
     const bool live = r < a.rows;
     if (which == 2) {                      // packed qkv: v += bias_v (block-uniform branch)
-        if (!live) return;
-        // the q/k lane layout over the row's heads; every load before the
-        // first store (loads and stores share vmcnt on gfx9)
-        T* __restrict__ vr = static_cast<T*>(a.v) + r * a.in_stride;
+        // the q/k lane layout over the row's heads, bias_v staged in LDS once
+        // per block; every load before the first store (loads and stores
+        // share vmcnt on gfx9)
+        T* __restrict__ vr = static_cast<T*>(a.v) + (live ? r : a.rows - 1) * a.in_stride;
         float vv[NG][E];
 #pragma unroll
         for (int it = 0; it < NG; ++it) {
             const int hh = 4 * it + g;
             L::load(vr + (int64_t)(hh < H ? hh : H - 1) * D, m, vv[it]);
         }
+        for (int i = threadIdx.x; i < HD / 4; i += W * 64)
+            reinterpret_cast<float4*>(bs)[i] = reinterpret_cast<const float4*>(a.bias_v)[i];
+        lds_barrier();
+        if (!live) return;
 #pragma unroll
         for (int it = 0; it < NG; ++it) {
             const int hh = 4 * it + g;
             if (hh < H) {
                 float bv[E];
-                L::params(a.bias_v + (int64_t)hh * D, m, bv);
+                L::params(&bs[hh * D], m, bv);
 #pragma unroll
                 for (int i = 0; i < E; ++i) vv[it][i] = add_rn(vv[it][i], bv[i]);
             }
@@ -115,8 +120,14 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
     }
 
+    // gamma * scale and the bias, staged in LDS once per block
+    const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
     if (gamma != nullptr) {
         for (int i = threadIdx.x; i < HD; i += W * 64) gs[i] = gamma[i] * a.rms_scale;
+    }
+    if (bias != nullptr) {
+        for (int i = threadIdx.x; i < HD / 4; i += W * 64)
+            reinterpret_cast<float4*>(bs)[i] = reinterpret_cast<const float4*>(bias)[i];
     }
 
     float pc[P], ps[P];
@@ -137,12 +148,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         }
     }
 
-    if (gamma != nullptr) {
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS stores are done
-        __builtin_amdgcn_s_barrier();
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
+    if (stage) lds_barrier();
     if (!live) return;
 
 #pragma unroll
@@ -151,7 +157,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         const bool valid = hh < H;
         if (bias != nullptr && valid) {
             float bv[E];
-            L::params(bias + (int64_t)hh * D, m, bv);
+            L::params(&bs[hh * D], m, bv);
 #pragma unroll
             for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
         }
