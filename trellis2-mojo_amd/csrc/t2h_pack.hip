@@ -146,14 +146,19 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
         }
     }
 
-    // The transposed path fetches head z + 1 before it stores head z, so a
-    // block's loads overlap its own stores.
+    // The transposed path fetches head z + 1 (rows and the head's bias and
+    // gamma) before it stores head z, so a block's loads overlap its own
+    // stores and no parameter load waits for them (loads and stores share
+    // vmcnt on gfx9).
     RawRow<T, D> raw[kPackIters];
+    float bv[E], gv[E];
     auto fetch = [&](int z) {
         if (a.rows > 0) {
 #pragma unroll
             for (int it = 0; it < kPackIters; ++it) raw[it].load(in + rl[it] * a.in_stride + (int64_t)z * D, m);
         }
+        if (bias != nullptr) L::params(bias + z * D, m, bv);
+        if (gamma != nullptr) L::params(gamma + z * D, m, gv);
     };
     if constexpr (KT) fetch(hg * order.hpb);
     for (int zi = 0; zi < order.hpb; ++zi) {
@@ -169,12 +174,10 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
 #pragma unroll
                 for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
         }
-        float bv[E], gv[E];
-        if (bias != nullptr) L::params(bias + z * D, m, bv);
+        float gsc[E];
         if (gamma != nullptr) {
-            L::params(gamma + z * D, m, gv);
 #pragma unroll
-            for (int i = 0; i < E; ++i) gv[i] *= a.rms_scale;
+            for (int i = 0; i < E; ++i) gsc[i] = gv[i] * a.rms_scale;
         }
 #pragma unroll
         for (int it = 0; it < kPackIters; ++it) {
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
                 const float ss = row16_sum(sum_sq<E>(x));
                 const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
 #pragma unroll
-                for (int i = 0; i < E; ++i) x[i] = (x[i] * rn) * gv[i];
+                for (int i = 0; i < E; ++i) x[i] = (x[i] * rn) * gsc[i];
             }
             if (rope) {
 #pragma unroll
