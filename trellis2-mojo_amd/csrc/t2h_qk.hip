@@ -105,12 +105,32 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     const float* __restrict__ bias = which == 0 ? a.bias_q : a.bias_k;
     const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
 
+    // 16-bit rows: the slot's frequency and the block's gamma / bias values
+    // are loaded before the row loads, so the phase and the LDS staging wait
+    // for them alone and run while the rows are in flight (MI355X, config 5:
+    // 414 -> 401 us). f32 keeps its parameter loads after the row loads:
+    // there the early order left the row loads behind an extra wait (config
+    // 2: 17.7 -> 31.9 us).
+    constexpr bool kEarly = sizeof(T) == 2;
     const int my_slot = lane % HALF;
     const int my_axis = tab.axis[my_slot];
+    const float my_freq = kEarly ? tab.freq[my_slot] : 0.0f;
     const bool coord_pos = a.use_rope && a.phases == nullptr && a.coords != nullptr;
     float cpos = 0.0f;
     if (live && coord_pos && my_axis >= 0) cpos = (float)a.coords[r * a.coord_cols + 1 + my_axis];
 
+    // gamma * scale and the bias, staged in LDS once per block
+    constexpr int KP = (NG * D + W * 64 - 1) / (W * 64);   // parameter float4s per thread
+    const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
+    float4 gl[KP], bl[KP];
+    if constexpr (kEarly) {
+#pragma unroll
+        for (int k = 0; k < KP; ++k) {
+            const int i = threadIdx.x + k * W * 64;
+            if (gamma != nullptr && i < HD / 4) gl[k] = reinterpret_cast<const float4*>(gamma)[i];
+            if (bias != nullptr && i < HD / 4) bl[k] = reinterpret_cast<const float4*>(bias)[i];
+        }
+    }
     const int64_t rl = live ? r : a.rows - 1;   // dead waves load a valid row, store nothing
     float v[NG][E];
 #pragma unroll
@@ -119,15 +139,24 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         const int hl = hh < H ? hh : H - 1;
         L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
     }
-
-    // gamma * scale and the bias, staged in LDS once per block
-    const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
-    if (gamma != nullptr) {
-        for (int i = threadIdx.x; i < HD; i += W * 64) gs[i] = gamma[i] * a.rms_scale;
-    }
-    if (bias != nullptr) {
-        for (int i = threadIdx.x; i < HD / 4; i += W * 64)
-            reinterpret_cast<float4*>(bs)[i] = reinterpret_cast<const float4*>(bias)[i];
+    if constexpr (kEarly) {
+#pragma unroll
+        for (int k = 0; k < KP; ++k) {
+            const int i = threadIdx.x + k * W * 64;
+            if (gamma != nullptr && i < HD / 4) {
+                const float sc = a.rms_scale;
+                reinterpret_cast<float4*>(gs)[i] = make_float4(gl[k].x * sc, gl[k].y * sc, gl[k].z * sc, gl[k].w * sc);
+            }
+            if (bias != nullptr && i < HD / 4) reinterpret_cast<float4*>(bs)[i] = bl[k];
+        }
+    } else {
+        if (gamma != nullptr) {
+            for (int i = threadIdx.x; i < HD; i += W * 64) gs[i] = gamma[i] * a.rms_scale;
+        }
+        if (bias != nullptr) {
+            for (int i = threadIdx.x; i < HD / 4; i += W * 64)
+                reinterpret_cast<float4*>(bs)[i] = reinterpret_cast<const float4*>(bias)[i];
+        }
     }
 
     float pc[P], ps[P];
@@ -139,7 +168,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
             float pos[T2H_MAX_POS_DIM] = {cpos, cpos, cpos, cpos};
             if (!coord_pos) src.get(live ? r : 0, pos);
             float c, s;
-            slot_phase(pos, my_axis, tab.freq[my_slot], c, s);
+            slot_phase(pos, my_axis, kEarly ? my_freq : tab.freq[my_slot], c, s);
 #pragma unroll
             for (int t = 0; t < P; ++t) {
                 pc[t] = lane_bcast(c, L::slot(m, t));
