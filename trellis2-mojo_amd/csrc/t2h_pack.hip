@@ -272,21 +272,28 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     const float* __restrict__ gamma = which == 0 ? a.gamma_q : which == 1 ? a.gamma_k : nullptr;
     const bool rope = a.use_rope && which < 2 && a.rows > 0;   // no rows: all pads
 
+    // 16-bit rows: the slot's frequency and the tensor's gamma and bias
+    // values are loaded before the row loads, so the phase and the LDS
+    // staging wait for them alone (as in qk_tile_kernel); f32 stages its
+    // parameters after the row loads.
+    constexpr bool kEarly = sizeof(T) == 2;
     const int my_slot = lane % HALF;
     const int my_axis = tab.axis[my_slot];
+    const float my_freq = kEarly ? tab.freq[my_slot] : 0.0f;
     const bool coord_pos = rope && a.phases == nullptr && a.coords != nullptr;
     float cpos = 0.0f;
     if (live && coord_pos && my_axis >= 0) cpos = (float)a.coords[r * a.coord_cols + 1 + my_axis];
 
-    // The tensor's gamma and bias rows, staged in LDS once per block; their
-    // loads go out before the row loads so the staging waits for them alone.
+    // the tensor's gamma and bias rows, staged in LDS once per block
     const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
     float gl[KP], bl[KP];
+    if constexpr (kEarly) {
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
-        const int i = threadIdx.x + k * kRowBlock;
-        if (gamma != nullptr && i < H * D) gl[k] = gamma[i];
-        if (bias != nullptr && i < H * D) bl[k] = bias[i];
+        for (int k = 0; k < KP; ++k) {
+            const int i = threadIdx.x + k * kRowBlock;
+            if (gamma != nullptr && i < H * D) gl[k] = gamma[i];
+            if (bias != nullptr && i < H * D) bl[k] = bias[i];
+        }
     }
     const int64_t rl = live ? r : (a.rows > 0 ? a.rows - 1 : 0);
     float v[NG][E];
@@ -303,11 +310,18 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
 #pragma unroll
             for (int i = 0; i < E; ++i) v[it][i] = 0.0f;
     }
+    if constexpr (kEarly) {
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
-        const int i = threadIdx.x + k * kRowBlock;
-        if (gamma != nullptr && i < H * D) gs[i] = gl[k] * a.rms_scale;
-        if (bias != nullptr && i < H * D) bs[i] = bl[k];
+        for (int k = 0; k < KP; ++k) {
+            const int i = threadIdx.x + k * kRowBlock;
+            if (gamma != nullptr && i < H * D) gs[i] = gl[k] * a.rms_scale;
+            if (bias != nullptr && i < H * D) bs[i] = bl[k];
+        }
+    } else {
+        for (int i = threadIdx.x; i < H * D; i += kRowBlock) {
+            if (gamma != nullptr) gs[i] = gamma[i] * a.rms_scale;
+            if (bias != nullptr) bs[i] = bias[i];
+        }
     }
     float pc[P], ps[P];
     if (rope) {
@@ -321,7 +335,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
                 src.get(rl, pos);
             }
             float c, sn;
-            slot_phase(pos, my_axis, tab.freq[my_slot], c, sn);
+            slot_phase(pos, my_axis, kEarly ? my_freq : tab.freq[my_slot], c, sn);
 #pragma unroll
             for (int t = 0; t < P; ++t) {
                 pc[t] = lane_bcast(c, L::slot(m, t));
