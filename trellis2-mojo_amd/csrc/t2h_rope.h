@@ -31,6 +31,14 @@ struct PosSource {
     }
 };
 
+// Axis of rotary slot p (< head_dim / 2): p / freq_dim for the pos_dim *
+// freq_dim rotated slots, -1 (identity) for the pad slots; the same mapping
+// as the host's slot table, computed without a load so that a kernel can
+// issue its coordinate load at once.
+__device__ __forceinline__ int slot_axis(int p, int freq_dim, int pos_dim) {
+    return (freq_dim > 0 && p < freq_dim * pos_dim) ? p / freq_dim : -1;
+}
+
 __device__ __forceinline__ float pick_axis(const float* pos, int ax) {
     return ax == 0 ? pos[0] : ax == 1 ? pos[1] : ax == 2 ? pos[2] : pos[3];
 }
