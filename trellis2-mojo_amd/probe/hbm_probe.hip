@@ -288,6 +288,36 @@ int launch_narrow(const void* s, void* d, const float*, int64_t rows, hipStream_
     return (int)hipGetLastError();
 }
 
+// Cache-policy bits of the 16-byte loads and stores, in the slab copy shape
+// (one vector per thread, 4 rows of one 1 KB column piece per block, 2-D
+// grid). Buffer instructions carry the bits as an immediate: bit 0 sc0,
+// bit 1 nt, bit 4 sc1. Each block's buffer descriptors start at its first
+// row and span its rows, so the 32-bit offsets stay small.
+template <int LA, int SA>
+__global__ __launch_bounds__(256) void policy_probe(void* src, void* dst, int64_t rows) {
+    constexpr int64_t kRowBytes = (int64_t)kVpr * 16;
+    const int64_t r0 = (int64_t)blockIdx.y * 4;
+    const int w = (int)(threadIdx.x >> 6);
+    const int nr = (int)(rows - r0 < 4 ? rows - r0 : 4);
+    const int wl = w < nr ? w : nr - 1;
+    const int c = (int)blockIdx.x * 64 + (int)(threadIdx.x & 63);
+    const int bytes = nr * (int)kRowBytes;
+    const __amdgpu_buffer_rsrc_t s =
+        __builtin_amdgcn_make_buffer_rsrc(static_cast<char*>(src) + r0 * kRowBytes, 0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t d =
+        __builtin_amdgcn_make_buffer_rsrc(static_cast<char*>(dst) + r0 * kRowBytes, 0, bytes, 0x00020000);
+    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(s, (wl * kVpr + c) * 16, 0, LA);
+    v.x ^= 0x3C003C00u;
+    if (w < nr) __builtin_amdgcn_raw_buffer_store_b128(v, d, (w * kVpr + c) * 16, 0, SA);
+}
+
+template <int LA, int SA>
+int launch_policy(const void* s, void* d, const float*, int64_t rows, hipStream_t st) {
+    hipLaunchKernelGGL((policy_probe<LA, SA>), dim3(kVpr / 64, (unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                       const_cast<void*>(s), d, rows);
+    return (int)hipGetLastError();
+}
+
 // The same probe writing its output over its input (each thread stores
 // exactly the vectors it loaded).
 template <Launch F>
@@ -335,6 +365,11 @@ const Probe kProbes[] = {
     {"narrow copy wave per row x8", launch_narrow<0>}, {"narrow copy wave per row x4", launch_narrow<4>},
     {"narrow copy 3 waves per row x4", launch_narrow<1>}, {"narrow copy 3 waves per row x2", launch_narrow<3>},
     {"narrow copy 1 KB piece x4 rows", launch_narrow<2>},
+    // cache-policy bits (load / store): 0 none, 2 nt, 16 sc1, 17 sc0 sc1, 18 nt sc1
+    {"policy copy L nt S nt", launch_policy<2, 2>},   {"policy copy L - S -", launch_policy<0, 0>},
+    {"policy copy L - S nt", launch_policy<0, 2>},    {"policy copy L nt S -", launch_policy<2, 0>},
+    {"policy copy L nt S nt sc1", launch_policy<2, 18>}, {"policy copy L nt S sc0 sc1", launch_policy<2, 17>},
+    {"policy copy L nt sc1 S nt", launch_policy<18, 2>}, {"policy copy L sc1 S sc1", launch_policy<16, 16>},
 };
 
 }  // namespace
