@@ -699,6 +699,44 @@ def chain_sweep(torch, dev, steps):
     print(json.dumps({"chain_sweep": res, "bytes_per_token": 52240}), flush=True)
 
 
+# The sources each chain op's kernel is built from (its launcher included).
+TRAFFIC_SOURCES = {
+    "ln_modulate": ["t2h_norm.hip"],
+    "qk_rmsnorm_rope": ["t2h_qk.hip", "t2h_rope.h"],
+    "gelu_tanh_bias": ["t2h_eltwise.hip"],
+    "gate_residual": ["t2h_eltwise.hip"],
+}
+TRAFFIC_COMMON = ["t2h_device.h", "t2h_internal.h"]
+
+
+def traffic_sources_sha(op):
+    """sha256 over the csrc files `op`'s kernel is built from, in a fixed order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES[op] + TRAFFIC_COMMON:
+        with open(os.path.join(ROOT, "trellis2-mojo_amd", "csrc", f), "rb") as fh:
+            h.update(f.encode() + b"\0" + fh.read())
+    return h.hexdigest()
+
+
+def measured_traffic(op, path=None):
+    """(HBM bytes per launch of `op` from profiles/traffic_c5.json, stale).
+    The file records the sources' sha256 at measurement time; when the
+    kernel's sources differ now, the figure belongs to another build and
+    is not reported (None, True)."""
+    path = path or os.path.join(ROOT, "profiles", "traffic_c5.json")
+    try:
+        rec = json.load(open(path))
+    except (OSError, ValueError):
+        return None, False
+    if op not in rec:
+        return None, False
+    if rec.get("_sources_sha256", {}).get(op) != traffic_sources_sha(op):
+        return None, True
+    return rec[op], False
+
+
 def hbm_probes(torch, dev, steps, rows=201436, only=None):
     """The streaming probes of trellis2-mojo_amd/probe/hbm_probe.hip on the
     config-5 GELU tensor (f16 [rows, 6144], 201,436 rows by default): what
@@ -801,16 +839,13 @@ def main():
             f"({chain.bytes[n]/t_ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
     dom = "gelu_tanh_bias"
     ach = per_op[dom]["gbs"]
-    traffic = None
-    tr_path = os.path.join(ROOT, "profiles", "traffic_c5.json")
-    if os.path.exists(tr_path):
-        try:
-            traffic = json.load(open(tr_path)).get(dom)
-        except Exception:
-            traffic = None
+    traffic, stale = measured_traffic(dom)
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": chain.bytes[dom], "launch_us": round(per_op[dom]["us"], 2)}
+    if stale:
+        roofline["traffic_stale"] = True
+        log(f"roofline.traffic: profiles/traffic_c5.json was measured on other {dom} sources; reported as null")
 
     cpu = None
     if not args.no_cpu:
