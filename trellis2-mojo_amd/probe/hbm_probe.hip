@@ -288,6 +288,83 @@ int launch_narrow(const void* s, void* d, const float*, int64_t rows, hipStream_
     return (int)hipGetLastError();
 }
 
+// LayerNorm + modulate over rows of 1536 f16 with one 16-byte vector per
+// lane: 3 waves per row, RPB rows per block. Each wave reduces its 512
+// values to (sum, sum of squares about its own mean); the block's waves swap
+// those through LDS behind one barrier (which also covers the staging of
+// the shift and scale rows, f32 [2][1536] from `par`), and each combines its
+// row's three pairs (Chan et al.'s pairwise update) into the row's mean and
+// variance.
+__device__ __forceinline__ float probe_wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+template <int RPB>
+__global__ __launch_bounds__(RPB * 192) void lnrow_probe(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                         const float* __restrict__ par, int64_t rows) {
+    __shared__ float4 ps[768];
+    __shared__ float2 part[RPB * 3];
+    const int wave = (int)(threadIdx.x >> 6);
+    const int lane = (int)(threadIdx.x & 63);
+    const int64_t r = (int64_t)blockIdx.x * RPB + wave / 3;
+    const int piece = wave % 3;
+    const int64_t rl = r < rows ? r : rows - 1;
+    const u32x4 w = __builtin_nontemporal_load(src + rl * kNarrowVpr + piece * 64 + lane);
+    for (int i = (int)threadIdx.x; i < 768; i += RPB * 192) ps[i] = reinterpret_cast<const float4*>(par)[i];
+    const uint32_t in[4] = {w.x, w.y, w.z, w.w};
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(in[i] & 0xFFFFu));
+        x[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(in[i] >> 16));
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += x[i];
+    sum = probe_wave_sum(sum);
+    const float mw = sum * (1.0f / 512.0f);
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q += (x[i] - mw) * (x[i] - mw);
+    q = probe_wave_sum(q);
+    if (lane == 0) part[wave] = make_float2(sum, q);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (r >= rows) return;
+    const int w0 = wave / 3 * 3;
+    const float2 p0 = part[w0], p1 = part[w0 + 1], p2 = part[w0 + 2];
+    const float mean = (p0.x + p1.x + p2.x) * (1.0f / 1536.0f);
+    const float d0 = p0.x * (1.0f / 512.0f) - mean, d1 = p1.x * (1.0f / 512.0f) - mean,
+                d2 = p2.x * (1.0f / 512.0f) - mean;
+    const float m2 = p0.y + p1.y + p2.y + 512.0f * (d0 * d0 + d1 * d1 + d2 * d2);
+    const float inv = __builtin_amdgcn_rsqf(m2 * (1.0f / 1536.0f) + 1e-6f);
+    const int c4 = (piece * 512 + lane * 8) / 4;
+    const float4 sh0 = ps[c4], sh1 = ps[c4 + 1], sc0 = ps[384 + c4], sc1 = ps[384 + c4 + 1];
+    const float sh[8] = {sh0.x, sh0.y, sh0.z, sh0.w, sh1.x, sh1.y, sh1.z, sh1.w};
+    const float sc[8] = {sc0.x, sc0.y, sc0.z, sc0.w, sc1.x, sc1.y, sc1.z, sc1.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = (x[2 * i] - mean) * inv * (1.0f + sc[2 * i]) + sh[2 * i];
+        const float hi = (x[2 * i + 1] - mean) * inv * (1.0f + sc[2 * i + 1]) + sh[2 * i + 1];
+        o[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    }
+    __builtin_nontemporal_store((u32x4){o[0], o[1], o[2], o[3]}, dst + r * kNarrowVpr + piece * 64 + lane);
+}
+
+template <int RPB>
+int launch_lnrow(const void* s, void* d, const float* par, int64_t rows, hipStream_t st) {
+    const int64_t nrows = rows * 4;   // [rows, 6144] as [4 * rows, 1536]
+    hipLaunchKernelGGL((lnrow_probe<RPB>), dim3((unsigned)((nrows + RPB - 1) / RPB)), dim3(RPB * 192), 0, st,
+                       static_cast<const u32x4*>(s), static_cast<u32x4*>(d), par, nrows);
+    return (int)hipGetLastError();
+}
+
 // Cache-policy bits of the 16-byte loads and stores, in the slab copy shape
 // (one vector per thread, 4 rows of one 1 KB column piece per block, 2-D
 // grid). Buffer instructions carry the bits as an immediate: bit 0 sc0,
@@ -365,6 +442,9 @@ const Probe kProbes[] = {
     {"narrow copy wave per row x8", launch_narrow<0>}, {"narrow copy wave per row x4", launch_narrow<4>},
     {"narrow copy 3 waves per row x4", launch_narrow<1>}, {"narrow copy 3 waves per row x2", launch_narrow<3>},
     {"narrow copy 1 KB piece x4 rows", launch_narrow<2>},
+    {"narrow LN+modulate 3 waves per row x4", launch_lnrow<4>},
+    {"narrow LN+modulate 3 waves per row x2", launch_lnrow<2>},
+    {"narrow LN+modulate 3 waves per row x1", launch_lnrow<1>},
     // cache-policy bits (load / store): 0 none, 2 nt, 16 sc1, 17 sc0 sc1, 18 nt sc1
     {"policy copy L nt S nt", launch_policy<2, 2>},   {"policy copy L - S -", launch_policy<0, 0>},
     {"policy copy L - S nt", launch_policy<0, 2>},    {"policy copy L nt S -", launch_policy<2, 0>},
