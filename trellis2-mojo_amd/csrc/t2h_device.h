@@ -155,6 +155,40 @@ template <typename T> __device__ __forceinline__ float ld1(const T* p) { return 
 template <> __device__ __forceinline__ float ld1<__bf16>(const __bf16* p) {
     return bf16_bits_to_f32(__builtin_bit_cast(uint16_t, *p));
 }
+
+// Streams of many non-temporal 16-byte loads run faster on MI355X when a
+// small share of the loads (one of a row's three 1 KB pieces in LN, one of a
+// gated-residual thread's eight) uses the default cache policy instead:
+// LN + modulate 201 -> 188 us, the config-5 chain 1,628 -> 1,601 us. All
+// non-temporal, or all cached, is slower. Launches that move less than
+// T2H_CACHED_SHARE_MIN bytes keep every load non-temporal: streams that fit
+// the 256 MB infinity cache read slower with the share when the cache holds
+// other dirty data.
+#ifndef T2H_CACHED_SHARE_MIN
+#define T2H_CACHED_SHARE_MIN (int64_t(512) << 20)
+#endif
+
+// E elements of T (E * sizeof(T) == 16) at element `off` of a wave-uniform
+// `row` of `n` elements, as f32, with the default (cached) policy: a buffer
+// load, a distinct instruction that the compiler does not merge with a
+// non-temporal load of the same address under a runtime condition.
+template <typename T, int E>
+__device__ __forceinline__ void load_elems_cached(const T* row, int64_t off, int64_t n, float* f) {
+    if constexpr (E * sizeof(T) != 16) {   // other widths: ordinary cached loads
+#pragma unroll
+        for (int i = 0; i < E; ++i) f[i] = ld1(row + off + i);
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), 0, (int)(n * (int64_t)sizeof(T)), 0x00020000);
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off * (int64_t)sizeof(T)), 0, 0);
+    constexpr int WN = Word<T>::N;
+    Word<T>::unpack(w.x, f + 0 * WN);
+    Word<T>::unpack(w.y, f + 1 * WN);
+    Word<T>::unpack(w.z, f + 2 * WN);
+    Word<T>::unpack(w.w, f + 3 * WN);
+}
+
 template <typename T> __device__ __forceinline__ void st1(T* p, float v) { *p = (T)v; }
 template <> __device__ __forceinline__ void st1<__bf16>(__bf16* p, float v) {
     *p = __builtin_bit_cast(__bf16, (uint16_t)f32_to_bf16_bits(v));

@@ -206,7 +206,13 @@ __global__ __launch_bounds__(1024) void gate_res_kernel(EltArgs a) {
     for (int k = 0; k < kRpt; ++k) {
         const int64_t off = t.row(k) * a.cols + t.col0;
         ld<T, V>(h + off, hv[k]);
-        ld<T, V>(xs + off, xv[k]);
+        // large launches: the residual's first row of the tile with the
+        // default cache policy (a buffer load: not merged with its
+        // non-temporal twins)
+        if (V > 1 && k == 0 && a.cached)
+            load_elems_cached<T, V>(xs + t.row(k) * a.cols, t.col0, a.cols, xv[k]);
+        else
+            ld<T, V>(xs + off, xv[k]);
     }
 #pragma unroll
     for (int k = 0; k < kRpt; ++k) {
@@ -447,8 +453,9 @@ hipError_t act_typed(const EltArgs& a, hipStream_t s) {
 }
 
 template <typename T>
-hipError_t gate_res_typed(const EltArgs& a, hipStream_t s) {
+hipError_t gate_res_typed(EltArgs a, hipStream_t s) {
     constexpr int V = kPack<T>;
+    a.cached = a.rows * (int64_t)a.cols * (int64_t)sizeof(T) * 3 >= T2H_CACHED_SHARE_MIN;
     if (vec_ok<T>(a)) return tile_launch<V>(gate_res_kernel<T, V>, a, s);
     return tile_launch<1>(gate_res_kernel<T, 1>, a, s);
 }

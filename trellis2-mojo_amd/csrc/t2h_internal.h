@@ -38,6 +38,7 @@ struct LnArgs {
     int32_t dtype;
     BatchArgs batch;
     int64_t fper;        // logical blocks per front (set at launch)
+    int32_t cached;      // fast path: first row piece with the cached policy (set at launch)
 };
 
 // Per-slot RoPE table, passed by value as a kernel argument: slot p rotates
@@ -215,6 +216,7 @@ struct EltArgs {
     int64_t fper;          // logical blocks per front (set at launch)
     int32_t block_threads; // the launch's block width (set at launch): read from the
                            // arguments, since blockDim.x costs a vector load per wave
+    int32_t cached;        // gated residual: a tile's first residual row cached (set at launch)
 };
 
 // Grid of nblocks blocks. A dispatch counts work-items in 32 bits per grid

@@ -28,6 +28,7 @@ constexpr int kWavesPerBlock = T2H_LN_WAVES;   // fast path: rows per block
 constexpr int kFastBlock = 64 * kWavesPerBlock;
 constexpr int kBlock = 256;                      // generic path
 
+
 // y = LN epilogue of one centred value d = x - mean (f32), in the reference's
 // order: n = d * inv_std, then n * (1 + scale) + shift (pb holds the already
 // rounded 1 + scale) or n * w + b.
@@ -71,10 +72,18 @@ __global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
     // 1. the row loads, all in flight before anything else
     float v[NCH][E];
     float hv[NCH][E];
+    // large launches: the first 1 KB piece with the default cache policy,
+    // the rest non-temporal (a buffer load: not merged with its non-temporal
+    // twins)
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
-        if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
+        if (c == 0 && a.cached) {
+            load_elems_cached<T, E>(x + base, (c * 64 + lane) * E, C, v[c]);
+            if (JOIN) load_elems_cached<T, E>(h + base, (c * 64 + lane) * E, C, hv[c]);
+        } else {
+            load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
+            if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
+        }
     }
 
     // 2. stage the parameter rows of the block's first row's batch in LDS
@@ -250,6 +259,7 @@ template <typename T, int NCH, bool JOIN>
 hipError_t launch_fast(LnArgs a, hipStream_t s) {
     const int64_t grid = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
     a.fper = front_per(grid);
+    a.cached = a.rows * (int64_t)a.cols * (int64_t)sizeof(T) * (JOIN ? 4 : 2) >= T2H_CACHED_SHARE_MIN;
     hipLaunchKernelGGL((ln_rows_kernel<T, NCH, JOIN>), grid_1d(front_grid(grid)), dim3(kFastBlock), 0, s, a);
     return hipGetLastError();
 }
