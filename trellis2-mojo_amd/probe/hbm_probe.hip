@@ -24,6 +24,14 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kVpr = 768;   // 16-byte vectors per row
 
+// An empty asm that claims to read `dep` and rewrite `x`: the compiler must
+// wait for the load that produced `dep` before it uses `x`, and `x` keeps its
+// value.
+template <typename X>
+__device__ __forceinline__ void fake_dep(X& x, uint32_t dep) {
+    asm volatile("" : "+v"(x) : "v"(dep));
+}
+
 __device__ __forceinline__ float gelu(float v) {
     constexpr float k0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
     constexpr float k1 = k0 * 0.044715f;
@@ -191,7 +199,8 @@ __global__ __launch_bounds__(WPR * RPB * 64) void slab_probe(const u32x4* __rest
     static_assert(RPB >= 2 && 12 % WPR == 0, "shape");
     constexpr int S = 12 / WPR;       // column slabs per row
     constexpr int SV = WPR * 64;      // 16-byte vectors per slab row
-    __shared__ float4 bl[KIND == 1 ? 2 * SV : 1];
+    constexpr bool kBias = KIND == 1 || KIND == 3;   // KIND 2 / 3: copy / gelu+bias behind a lead load
+    __shared__ float4 bl[kBias ? 2 * SV : 1];
     const int64_t b = P == 0 ? (int64_t)blockIdx.y * S + blockIdx.x
                              : (int64_t)(blockIdx.x % P) * per + blockIdx.x / P;
     if (b >= nb) return;   // block-uniform, before the barrier
@@ -202,10 +211,14 @@ __global__ __launch_bounds__(WPR * RPB * 64) void slab_probe(const u32x4* __rest
     const int64_t r = tile * RPB + wave / WPR;
     const int c = slab * SV + j;
     float4 bq = {0.f, 0.f, 0.f, 0.f};
-    if (KIND == 1 && threadIdx.x < 2 * SV) bq = reinterpret_cast<const float4*>(bias)[slab * 2 * SV + threadIdx.x];
-    const int64_t rl = r < rows ? r : rows - 1;
+    if (kBias && threadIdx.x < 2 * SV) bq = reinterpret_cast<const float4*>(bias)[slab * 2 * SV + threadIdx.x];
+    int64_t rl = r < rows ? r : rows - 1;
+    if (KIND >= 2) {   // the row load waits for a 4-byte load of the same vector
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(src + rl * kVpr + c);
+        fake_dep(rl, w0);
+    }
     u32x4 v = __builtin_nontemporal_load(src + rl * kVpr + c);
-    if (KIND == 1) {
+    if (kBias) {
         if (threadIdx.x < 2 * SV) bl[threadIdx.x] = bq;
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS stores are done
@@ -237,11 +250,28 @@ int launch_slab(const void* s, void* d, const float* bias, int64_t rows, hipStre
 //   MODE 2  4 waves on 4 rows of one 1 KB piece; consecutive blocks walk the 3 pieces
 //   MODE 3  3 waves per row, one vector per lane, 2 rows per block (6 waves)
 //   MODE 4  one wave per row, 3 vectors per lane, 4 rows per block
+//   MODE 5  MODE 0 whose row loads wait for one dependent 4-byte load of the
+//           row first (as the QK kernel's row loads wait for its coordinates)
+//   MODE 6  MODE 0 whose row loads wait for a 4-byte load of one word every
+//           wave reads (an L2 hit after the first: a delay, no prefetch)
+//   MODE 7  MODE 0 with the 4-byte loads of MODE 5 issued but not waited for
+//           (the prefetch without the delay)
+//   MODE 8  MODE 0 whose row loads wait for a 4-byte load of a separate
+//           16-byte-per-row array (the QK kernel's coordinates)
+//   MODE 9  MODE 7 with a 4-byte load in each of the row's three 1 KB pieces
+//   MODE 10 MODE 7 with the 4-byte load non-temporal
+//   MODE 11 MODE 7 with the 4-byte load in the row's second 1 KB piece
+//   MODE 12 MODE 0 with the row loads without the non-temporal bit
+//   MODE 13 MODE 0 with the first 1 KB piece's load without the non-temporal bit
 constexpr int kNarrowVpr = 192;
 template <int MODE>
-constexpr int narrow_waves() { return MODE == 0 ? 8 : MODE == 1 ? 12 : MODE == 3 ? 6 : 4; }
+constexpr bool narrow_wave_row() { return MODE == 0 || MODE == 4 || MODE >= 5; }
 template <int MODE>
-constexpr int narrow_rows() { return MODE == 0 ? 8 : MODE == 3 ? 2 : 4; }
+constexpr int narrow_waves() { return MODE == 0 || MODE >= 5 ? 8 : MODE == 1 ? 12 : MODE == 3 ? 6 : 4; }
+template <int MODE>
+constexpr int narrow_rows() { return MODE == 0 || MODE >= 5 ? 8 : MODE == 3 ? 2 : 4; }
+
+
 
 template <int MODE>
 __global__ __launch_bounds__(narrow_waves<MODE>() * 64) void narrow_probe(const u32x4* __restrict__ src,
@@ -249,12 +279,49 @@ __global__ __launch_bounds__(narrow_waves<MODE>() * 64) void narrow_probe(const 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int64_t b = blockIdx.x;
-    if (MODE == 0 || MODE == 4) {
+    if (narrow_wave_row<MODE>()) {
         const int64_t r = b * narrow_rows<MODE>() + wave;
-        const int64_t rl = r < rows ? r : rows - 1;
+        int64_t rl = r < rows ? r : rows - 1;
+        uint32_t w7 = 0;
+        if (MODE == 5 || MODE == 7) {
+            // a word of each of the row's first 64 vectors
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(src + rl * kNarrowVpr + lane);
+            if (MODE == 5) fake_dep(rl, w0);
+            else w7 = w0;   // consumed after the row loads
+        } else if (MODE == 9) {
+            const uint32_t* q = reinterpret_cast<const uint32_t*>(src + rl * kNarrowVpr + lane);
+            w7 = q[0] ^ q[256] ^ q[512];
+        } else if (MODE == 10) {
+            w7 = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + rl * kNarrowVpr + lane));
+        } else if (MODE == 11) {
+            w7 = *reinterpret_cast<const uint32_t*>(src + rl * kNarrowVpr + 64 + lane);
+        } else if (MODE == 6) {
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(src + lane);
+            fake_dep(rl, w0);
+        } else if (MODE == 8) {
+            // 16 bytes per row in the last 16 * rows bytes of the destination
+            // (written by the row stores only after this read, and rewritten by
+            // them: the probe's output is not checked)
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(dst + (rows * kNarrowVpr - rows) + rl);
+            fake_dep(rl, w0);
+        }
         u32x4 v[3];
+        const u32x4* q = src + rl * kNarrowVpr + lane;
+        if constexpr (MODE == 12) {
+            v[0] = q[0];
+            v[1] = q[64];
+            v[2] = q[128];
+        } else if constexpr (MODE == 13) {
+            v[0] = q[0];
+            v[1] = __builtin_nontemporal_load(q + 64);
+            v[2] = __builtin_nontemporal_load(q + 128);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 3; ++j) v[j] = __builtin_nontemporal_load(src + rl * kNarrowVpr + j * 64 + lane);
+            for (int j = 0; j < 3; ++j) v[j] = __builtin_nontemporal_load(q + j * 64);
+        }
+        // MODE 7, 9-11: the lead word is waited for with the row loads, not before them
+        if (MODE == 7 || (MODE >= 9 && MODE <= 11))
+            asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]) : "v"(w7));
         if (r < rows) {
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
@@ -438,10 +505,21 @@ const Probe kProbes[] = {
     {"slab gelu+bias 1x8 P8", launch_slab<1, 8, 1, 8>}, {"slab gelu+bias 4x4 P8", launch_slab<4, 4, 1, 8>},
     {"slab gelu+bias 1x4 2-D grid", launch_slab<1, 4, 1, 0>}, {"slab gelu+bias 1x2", launch_slab<1, 2, 1, 1>},
     {"slab copy 1x4 2-D grid", launch_slab<1, 4, 0, 0>},
+    {"slab copy 1x4 2-D grid lead load", launch_slab<1, 4, 2, 0>},
+    {"slab gelu+bias 1x4 2-D grid lead load", launch_slab<1, 4, 3, 0>},
     // 3 KB rows (1536 f16)
     {"narrow copy wave per row x8", launch_narrow<0>}, {"narrow copy wave per row x4", launch_narrow<4>},
     {"narrow copy 3 waves per row x4", launch_narrow<1>}, {"narrow copy 3 waves per row x2", launch_narrow<3>},
     {"narrow copy 1 KB piece x4 rows", launch_narrow<2>},
+    {"narrow copy wave per row x8 dependent lead load", launch_narrow<5>},
+    {"narrow copy wave per row x8 shared lead load", launch_narrow<6>},
+    {"narrow copy wave per row x8 lead load no wait", launch_narrow<7>},
+    {"narrow copy wave per row x8 side-array lead load", launch_narrow<8>},
+    {"narrow copy wave per row x8 lead load per piece", launch_narrow<9>},
+    {"narrow copy wave per row x8 nt lead load", launch_narrow<10>},
+    {"narrow copy wave per row x8 lead load second piece", launch_narrow<11>},
+    {"narrow copy wave per row x8 cached row loads", launch_narrow<12>},
+    {"narrow copy wave per row x8 first piece cached", launch_narrow<13>},
     {"narrow LN+modulate 3 waves per row x4", launch_lnrow<4>},
     {"narrow LN+modulate 3 waves per row x2", launch_lnrow<2>},
     {"narrow LN+modulate 3 waves per row x1", launch_lnrow<1>},
