@@ -72,14 +72,15 @@ __global__ __launch_bounds__(kFastBlock) void ln_rows_kernel(LnArgs a) {
     // 1. the row loads, all in flight before anything else
     float v[NCH][E];
     float hv[NCH][E];
-    // large launches: the first 1 KB piece with the default cache policy,
-    // the rest non-temporal (a buffer load: not merged with its non-temporal
-    // twins)
+    // large launches: x's first 1 KB piece with the default cache policy,
+    // the rest (h's pieces included: one cached load of six measured faster
+    // than two) non-temporal; a buffer load, not merged with its
+    // non-temporal twins
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         if (c == 0 && a.cached) {
             load_elems_cached<T, E>(x + base, (c * 64 + lane) * E, C, v[c]);
-            if (JOIN) load_elems_cached<T, E>(h + base, (c * 64 + lane) * E, C, hv[c]);
+            if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
         } else {
             load_elems<T, E, true>(x + base + (c * 64 + lane) * E, v[c]);
             if (JOIN) load_elems<T, E, true>(h + base + (c * 64 + lane) * E, hv[c]);
