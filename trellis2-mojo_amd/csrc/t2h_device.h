@@ -169,7 +169,8 @@ template <> __device__ __forceinline__ float ld1<__bf16>(const __bf16* p) {
 #endif
 
 // E elements of T (E * sizeof(T) == 16) at element `off` of a wave-uniform
-// `row` of `n` elements, as f32, with the default (cached) policy: a buffer
+// `row` of `n` elements (n * sizeof(T) <= INT32_MAX: the descriptor's size
+// and offset are 32-bit), as f32, with the default (cached) policy: a buffer
 // load, a distinct instruction that the compiler does not merge with a
 // non-temporal load of the same address under a runtime condition.
 template <typename T, int E>

@@ -455,7 +455,9 @@ hipError_t act_typed(const EltArgs& a, hipStream_t s) {
 template <typename T>
 hipError_t gate_res_typed(EltArgs a, hipStream_t s) {
     constexpr int V = kPack<T>;
-    a.cached = a.rows * (int64_t)a.cols * (int64_t)sizeof(T) * 3 >= T2H_CACHED_SHARE_MIN;
+    // the cached row loads address a row through a buffer descriptor: 32-bit byte offsets
+    a.cached = a.rows * (int64_t)a.cols * (int64_t)sizeof(T) * 3 >= T2H_CACHED_SHARE_MIN &&
+               (int64_t)a.cols * (int64_t)sizeof(T) <= INT32_MAX;
     if (vec_ok<T>(a)) return tile_launch<V>(gate_res_kernel<T, V>, a, s);
     return tile_launch<1>(gate_res_kernel<T, 1>, a, s);
 }
