@@ -51,12 +51,6 @@ def parse():
     p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
     p.add_argument("--sweep", action="store_true",
                    help="time the config-5 chain at several token counts and print their JSON")
-    p.add_argument("--probe", action="store_true",
-                   help="time the HBM streaming probes (lib/libhbm_probe.so) instead of the chain")
-    p.add_argument("--probe-rows", type=int, default=201436,
-                   help="rows of the f16 [rows, 6144] tensor the probes stream")
-    p.add_argument("--probe-only", default=None,
-                   help="comma-separated probe names to run (default: all)")
     return p.parse_args()
 
 
@@ -737,43 +731,6 @@ def measured_traffic(op, path=None):
     return rec[op], False
 
 
-def hbm_probes(torch, dev, steps, rows=201436, only=None):
-    """The streaming probes of trellis2-mojo_amd/probe/hbm_probe.hip on the
-    config-5 GELU tensor (f16 [rows, 6144], 201,436 rows by default): what
-    each access pattern and block shape reaches with nothing else in the
-    kernel. `only`: the probe names to run. Prints one JSON line."""
-    import ctypes
-
-    from t2h import _build
-
-    L = ctypes.CDLL(_build.PROBE_PATH)
-    L.hbm_probe_name.restype = ctypes.c_char_p
-    L.hbm_probe_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
-                                   ctypes.c_void_p]
-    cols = 6144
-    g = torch.Generator(device=dev).manual_seed(3)
-    src = torch.randn((rows, cols), generator=g, device=dev).half()
-    dst = torch.empty_like(src)
-    bias = torch.randn((cols,), generator=g, device=dev) * 0.02
-    st = torch.cuda.current_stream().cuda_stream
-    nbytes = 2 * rows * cols * 2
-    res = {}
-    names = [L.hbm_probe_name(i).decode() for i in range(L.hbm_probe_count())]
-    if only:
-        missing = [n for n in only if n not in names]
-        if missing:
-            raise SystemExit(f"unknown probe(s): {missing}")
-    for i, name in enumerate(names):
-        if only and name not in only:
-            continue
-        fn = lambda: L.hbm_probe_launch(i, src.data_ptr(), dst.data_ptr(), bias.data_ptr(), rows, st)
-        assert fn() == 0, name
-        ms = time_region(torch, fn, steps) / steps
-        res[name] = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / ms / 1e6, 1)}
-        log(f"  {name:<20s} {ms*1e3:8.1f} us {nbytes/ms/1e6:8.1f} GB/s ({nbytes/ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
-    print(json.dumps({"hbm_probes": res, "bytes_per_launch": nbytes}), flush=True)
-
-
 def main():
     args = parse()
     if args.gpus != 1:
@@ -788,10 +745,6 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     ops.device_init(0)
-    if args.probe:
-        hbm_probes(torch, dev, args.steps, args.probe_rows,
-                   [n.strip() for n in args.probe_only.split(",")] if args.probe_only else None)
-        return
     if args.sweep:
         chain_sweep(torch, dev, args.steps)
         return

@@ -18,7 +18,10 @@
  *     t2h_h_* functions take HOST pointers only.
  *   - `stream` is a hipStream_t (NULL = the default stream). Device entry
  *     points only enqueue work: no allocation, no synchronisation, no host
- *     reads of device data. They are stateless and reentrant.
+ *     reads of device data. They are stateless and reentrant, with one
+ *     exception: t2h_flow_euler_step_noalloc keeps its rescale statistics in
+ *     one scratch array per GPU, so its calls that overlap on one GPU (other
+ *     streams or threads) mix each other's statistics and are not reentrant.
  *   - `dtype` (T2H_F32 / T2H_F16 / T2H_BF16) is the storage type of the token
  *     tensors; all arithmetic is f32. Parameter vectors (shift, scale, gate,
  *     bias, gamma, weight) are always f32, as in the reference.

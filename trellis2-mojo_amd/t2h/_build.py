@@ -19,8 +19,6 @@ INCLUDE = os.path.join(REPO_ROOT, "include")
 BUILD_DIR = os.path.join(PKG_ROOT, "_build")
 LIB_DIR = os.path.join(PKG_ROOT, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libt2h.so")
-PROBE_SRC = os.path.join(PKG_ROOT, "probe", "hbm_probe.hip")
-PROBE_PATH = os.path.join(LIB_DIR, "libhbm_probe.so")   # bench.py --probe only; not part of libt2h
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -56,9 +54,6 @@ def build(verbose: bool = False) -> str:
     # emitted) fails the link here instead of the first dlopen on a GPU box
     logs.append(_run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *objs, "-o", tmp]))
     os.replace(tmp, LIB_PATH)
-    ptmp = PROBE_PATH + ".tmp"
-    logs.append(_run([HIPCC, *CFLAGS, "-shared", PROBE_SRC, "-o", ptmp]))
-    os.replace(ptmp, PROBE_PATH)
     if verbose:
         print("\n".join(l for l in logs if l.strip()))
     return LIB_PATH
