@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--settle-ms", type=float, default=400.0,
+                   help="GPU time of untimed chain steps before the steady-state windows")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline sample time")
     p.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1-4")
@@ -247,6 +249,66 @@ def time_region(torch, fn, steps):
     torch.cuda.synchronize()
     return s.elapsed_time(e)
 
+
+def steady_state(torch, chain, settle_ms, steps, rounds=3):
+    """The chain after settle_ms of untimed chain steps.
+    - steady: windows of `steps` whole chain steps (median of `rounds`);
+    - per_op (in-chain marginal time of each op): the same window with that
+      op left out, subtracted from the interleaved whole-chain window, so no
+      event sits inside a timed window (each event record between two kernels
+      adds a ~5.6 us gap, which a kernel trace shows);
+    - per_op_events: one window with an event between consecutive ops (each
+      interval includes one such gap)."""
+    t0 = time.perf_counter()
+    settled = 0.0
+    while settled < settle_ms:
+        settled += time_region(torch, chain.step, 20)
+        if time.perf_counter() - t0 > 10.0:
+            break
+    fns = {n: chain.op(n) for n in Chain.ORDER}
+
+    def without(skip):
+        rest = [fns[n] for n in Chain.ORDER if n != skip]
+
+        def run():
+            for f in rest:
+                f()
+        return run
+
+    full, left = [], {n: [] for n in Chain.ORDER}
+    for _ in range(rounds):
+        full.append(time_region(torch, chain.step, steps) / steps)
+        for n in Chain.ORDER:
+            left[n].append(time_region(torch, without(n), steps) / steps)
+    ms = statistics.median(full)
+    per_op = {}
+    for n in Chain.ORDER:
+        m = max(ms - statistics.median(left[n]), 1e-6)
+        per_op[n] = {"us": round(m * 1e3, 2), "bytes": chain.bytes[n], "gbs": round(chain.bytes[n] / m / 1e6, 1),
+                     "pct_of_peak": round(chain.bytes[n] / m / 1e6 / HBM_PEAK_GBS * 100, 2)}
+    order = [fns[n] for n in Chain.ORDER]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(order) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for k in range(steps):
+        e = ev[k]
+        e[0].record()
+        for i, fn in enumerate(order):
+            fn()
+            e[i + 1].record()
+    torch.cuda.synchronize()
+    per_ev = {}
+    for i, n in enumerate(Chain.ORDER):
+        ts = [ev[k][i].elapsed_time(ev[k][i + 1]) for k in range(steps)]
+        m = statistics.mean(ts)
+        per_ev[n] = {"us": round(m * 1e3, 2), "median_us": round(statistics.median(ts) * 1e3, 2),
+                     "gbs": round(chain.bytes[n] / m / 1e6, 1)}
+    gbs = chain.chain_bytes / ms / 1e6
+    return {"settle_ms": round(settled, 1), "steps": steps, "rounds": rounds, "us_per_step": round(ms * 1e3, 2),
+            "gbs": round(gbs, 1), "pct_of_peak": round(gbs / HBM_PEAK_GBS * 100, 2),
+            "tokens_per_s": round(chain.T / ms * 1e3),
+            "per_op_sum_us": round(sum(v["us"] for v in per_op.values()), 2), "per_op": per_op,
+            "per_op_events": per_ev,
+            "per_op_events_sum_us": round(sum(v["us"] for v in per_ev.values()), 2)}
 
 def time_op(torch, fn, reps, flush=None):
     """Median per-launch ms of one launch between two events. With `flush`,
@@ -770,6 +832,11 @@ def main():
         log(f"{args.op}: {ms/args.steps*1e3:.1f} us/launch, {nb/(ms/args.steps)/1e6:.1f} GB/s")
         return
 
+    # The first timed event pair of a process sets up the runtime's timestamp
+    # machinery (~50 ms, the GPU idle, in a kernel trace of a fresh process);
+    # done here, before the warm-up, that idle does not fall between the
+    # warm-up and the timed steps.
+    time_region(torch, lambda: None, 1)
     for _ in range(args.warmup):
         chain.step()
     torch.cuda.synchronize()
@@ -780,22 +847,38 @@ def main():
     log(f"chain: {ms_step*1e3:.1f} us/step, {gbs:.1f} GB/s ({gbs/HBM_PEAK_GBS*100:.1f}% of peak), "
         f"{tok_s/1e6:.1f} M tokens/s")
 
-    # per-op launch durations (same stream, same buffers), live
-    per_op = {}
+    # The same chain once the GPU has left its idle clocks: the first tens of
+    # milliseconds of load after a process starts run a few percent slower
+    # (kernel traces of a fresh process show every kernel of the first steps
+    # longer), so the window above can carry that ramp. The chain runs
+    # untimed for settle_ms of GPU time, then one window is timed whole
+    # (steady) and one with an event pair around every op (in-chain per-op
+    # durations; the events add a little to that window only).
+    steady = steady_state(torch, chain, args.settle_ms, max(args.steps, 30))
+    per_op = steady["per_op"]
+    log(f"steady state after {steady['settle_ms']:.0f} ms of chain steps: {steady['us_per_step']:.1f} us/step, "
+        f"{steady['gbs']:.1f} GB/s ({steady['pct_of_peak']:.1f}%); in-chain per-op sum "
+        f"{steady['per_op_sum_us']:.1f} us (event pairs: {steady['per_op_events_sum_us']:.1f} us)")
+    for n, v in per_op.items():
+        log(f"  in chain {n:<18s} {v['us']:8.1f} us  {v['gbs']:8.1f} GB/s ({v['gbs']/HBM_PEAK_GBS*100:5.1f}%)  "
+            f"event pair {steady['per_op_events'][n]['us']:8.1f} us")
+    # each op repeated on its own (same stream, same buffers), for comparison
+    alone = {}
     for n in Chain.ORDER:
         fn = chain.op(n)
         fn()
         reps = max(10, args.steps)
         t_ms = time_region(torch, fn, reps) / reps
-        per_op[n] = {"us": t_ms * 1e3, "bytes": chain.bytes[n], "gbs": chain.bytes[n] / t_ms / 1e6}
-        log(f"  {n:<18s} {t_ms*1e3:8.1f} us  {chain.bytes[n]/t_ms/1e6:8.1f} GB/s "
-            f"({chain.bytes[n]/t_ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
+        alone[n] = {"us": round(t_ms * 1e3, 2), "gbs": round(chain.bytes[n] / t_ms / 1e6, 1)}
     dom = "gelu_tanh_bias"
-    ach = per_op[dom]["gbs"]
+    dom_ev = steady["per_op_events"][dom]
+    ach = chain.bytes[dom] / dom_ev["us"] * 1e-3
     traffic, stale = measured_traffic(dom)
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
-                "bytes_per_launch": chain.bytes[dom], "launch_us": round(per_op[dom]["us"], 2)}
+                "bytes_per_launch": chain.bytes[dom], "launch_us": dom_ev["us"],
+                "timing": "mean in-chain launch between the HIP events around it on the launch stream, in the "
+                          "steady-state window (the interval includes one event-record gap)"}
     if stale:
         roofline["traffic_stale"] = True
         log(f"roofline.traffic: profiles/traffic_c5.json was measured on other {dom} sources; reported as null")
@@ -825,7 +908,10 @@ def main():
                                "f16 storage / f32 math",
                    "tokens": chain.T, "width": 1536, "heads": 12, "head_dim": 128, "hidden": 6144,
                    "grid": "128^3 thickened sphere shell", "bytes_per_token": 52240},
-        "per_op": {k: {"us": round(v["us"], 2), "gbs": round(v["gbs"], 1)} for k, v in per_op.items()},
+        "steady_state": {k: v for k, v in steady.items() if k not in ("per_op", "per_op_events")},
+        "per_op": per_op,
+        "per_op_events": steady["per_op_events"],
+        "per_op_alone": alone,
         "next_rows": extra,
         "roofline": roofline,
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",

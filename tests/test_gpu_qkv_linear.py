@@ -5,6 +5,9 @@ oracle's composition of the reference's chain: the qkv GEMM
 pack_q_z and pack_kv_z (gpu/attention.mojo:507-563, 566-594, 634-662, order
 983-1013).
 
+head_dim 128 (12 heads at width 1536, config 5's geometry) and head_dim 64
+(16 heads at width 1024, the reference's sparse SLat geometry).
+
 Bar: the f16 (bf16) storage tolerance of tests/_parity.py. The GEMM sums the
 same exact products in another order and the head's sum of squares is
 reduced in another order, both far below the storage rounding; pads are
@@ -145,17 +148,101 @@ def test_other_head_counts(dev, heads):
     assert_close(vh, wv, torch.float16, f"vh H={heads}")
 
 
+def _case_hd(seed, rows, heads, hd, k, dtype):
+    n = 3 * heads * hd
+    x = storage_round(orc.randn(seed, (rows, k)), dtype)
+    w = storage_round(orc.randn(seed + 1, (n, k), std=0.02), dtype)
+    bias = orc.randn(seed + 2, (n,), std=0.05)
+    gq = orc.randn(seed + 3, (heads, hd), mean=1.0, std=0.02)
+    gk = orc.randn(seed + 4, (heads, hd), mean=1.0, std=0.02)
+    return x, w, bias, gq, gk
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("k_transposed", [True, False])
+def test_head_dim_64_slat_sparse_coords(dev, dtype, k_transposed):
+    """The reference's sparse SLat geometry: width 1024 as 16 heads of 64
+    (gpu/attention.mojo:983-1013; tests/parity/parity_wp11_gpu_attn.mojo's
+    whole-block case), 2,369 sparse tokens with RoPE from their int coords,
+    padded to a multiple of 64. A wave's 128 features are two heads: each
+    head's sum of squares is 32 values per lane and one lane ^ 32 shuffle."""
+    heads, hd, k = 16, 64, 1024
+    coords, _ = workloads.config4()
+    coords = np.ascontiguousarray(coords[:2369])
+    rows = coords.shape[0]
+    mp = (rows + 63) // 64 * 64
+    x, w, bias, gq, gk = _case_hd(5600, rows, heads, hd, k, dtype)
+    phases = orc.rope_phases_from_coords(coords, hd, orc.rope_freqs(hd))
+    wq, wk, wv = orc.attn_pack(orc.linear(x, w), heads, hd, mp, mp, bias, gq, gk, phases)
+    qh, ko, vh = ops.qkv_linear_pack(to_dev(x, dev, dtype), to_dev(w, dev, dtype), heads, bias=to_dev(bias, dev),
+                                     gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), mp=mp, lp=mp,
+                                     freqs=nn.rope_freqs(hd), coords=to_dev(coords, dev),
+                                     k_transposed=k_transposed)
+    assert qh.shape == (heads, mp, hd) and vh.shape == (heads, mp, hd)
+    assert ko.shape == ((heads, hd, mp) if k_transposed else (heads, mp, hd))
+    assert_close(qh, wq, dtype, "qh")
+    assert_close(ko, wk if k_transposed else wk.transpose(0, 2, 1), dtype, "k")
+    assert_close(vh, wv, dtype, "vh")
+    assert not host(qh)[:, rows:].any() and not host(vh)[:, rows:].any()
+
+
+def test_head_dim_64_dense_grid(dev):
+    """16 x 64 heads at width 1024 on 2,048 dense tokens (the reference's L =
+    2048 whole-block case) with the uploaded phase table, and the same tokens
+    with positions from the grid index: both equal the oracle's chain, and
+    the grid path equals a device-built phase table bit for bit."""
+    heads, hd, k, rows = 16, 64, 1024, 2048
+    x, w, bias, gq, gk = _case_hd(5700, rows, heads, hd, k, torch.float16)
+    phases = orc.rope_phases_from_positions(orc.grid_positions(16)[:rows], hd, orc.rope_freqs(hd))
+    wq, wk, wv = orc.attn_pack(orc.linear(x, w), heads, hd, rows, rows, bias, gq, gk, phases)
+    xd, wd = to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16)
+    kw = dict(bias=to_dev(bias, dev), gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(hd))
+    qh, kt, vh = ops.qkv_linear_pack(xd, wd, heads, phases=to_dev(phases, dev), **kw)
+    assert_close(qh, wq, torch.float16, "qh")
+    assert_close(kt, wk, torch.float16, "kt")
+    assert_close(vh, wv, torch.float16, "vh")
+    a = ops.qkv_linear_pack(xd, wd, heads, grid_res=16, **kw)
+    b = ops.qkv_linear_pack(xd, wd, heads, phases=ops.rope_phases(rows, hd, nn.rope_freqs(hd), grid_res=16,
+                                                                   device=dev), **kw)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_head_dim_64_is_gemm_plus_pack(dev):
+    """head_dim 64 without bias, RMS and RoPE: the GEMM's f32 sums rounded
+    once and permuted into the two heads of each wave's features (bit
+    exact), both k layouts; 8 heads, ragged rows, pads."""
+    heads, hd, k, rows = 8, 64, 512, 700
+    x, w, _, _, _ = _case_hd(5800, rows, heads, hd, k, torch.float16)
+    xd, wd = to_dev(x, dev, torch.float16), to_dev(w, dev, torch.float16)
+    qkv = host(ops.linear(xd, wd, out_dtype=torch.float32)).reshape(rows, 3, heads, hd)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    for kt_layout in (True, False):
+        qh, ko, vh = ops.qkv_linear_pack(xd, wd, heads, use_rope=False, mp=768, lp=712, k_transposed=kt_layout)
+        assert np.array_equal(host(qh)[:, :rows],
+                              storage_round((qkv[:, 0] * scale).transpose(1, 0, 2), torch.float16))
+        kw = qkv[:, 1].transpose(1, 2, 0) if kt_layout else qkv[:, 1].transpose(1, 0, 2)
+        got_k = host(ko)[:, :, :rows] if kt_layout else host(ko)[:, :rows]
+        assert np.array_equal(got_k, storage_round(kw, torch.float16))
+        assert np.array_equal(host(vh)[:, :rows], storage_round(qkv[:, 2].transpose(1, 0, 2), torch.float16))
+        assert not host(qh)[:, rows:].any() and not host(vh)[:, rows:].any()
+        assert not (host(ko)[:, :, rows:] if kt_layout else host(ko)[:, rows:]).any()
+
+
 def test_zero_rows_and_errors(dev):
     w = torch.zeros((3 * H * D, C), dtype=torch.float16, device=dev)
     qh, kt, vh = ops.qkv_linear_pack(torch.zeros((0, C), dtype=torch.float16, device=dev), w, H, mp=64, lp=64,
                                      use_rope=False)
     assert not host(qh).any() and not host(kt).any() and not host(vh).any()
-    with pytest.raises(T2HError, match="head_dim must be 128"):
+    with pytest.raises(T2HError, match="head_dim must be 64 or 128"):
         ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev),
-                            torch.zeros((3 * H * 64, C), dtype=torch.float16, device=dev), H, use_rope=False)
-    with pytest.raises(T2HError, match="even heads"):
+                            torch.zeros((3 * H * 32, C), dtype=torch.float16, device=dev), H, use_rope=False)
+    with pytest.raises(T2HError, match="even for head_dim 128"):
         ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev),
                             torch.zeros((3 * 3 * D, C), dtype=torch.float16, device=dev), 3, use_rope=False)
+    with pytest.raises(T2HError, match="a multiple of 4 for 64"):
+        ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev),
+                            torch.zeros((3 * 6 * 64, C), dtype=torch.float16, device=dev), 6, use_rope=False)
     with pytest.raises(ValueError, match="lp % 8"):
         ops.qkv_linear_pack(torch.zeros((4, C), dtype=torch.float16, device=dev), w, H, mp=4, lp=4,
                             use_rope=False)

@@ -75,10 +75,12 @@ def test_step_rescale_dense(dev, t):
     assert max_err(xp, orc.flow_step(x, pred, t, tp)) <= 1e-5 / cc
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_step_rescale_varlen_config4(dev, dtype):
     """Varlen state: config-4 token rows (T = 39,804, two batches) x 32
-    latent channels, per-segment biased std (the shape stage, rescale 0.5)."""
+    latent channels, per-segment biased std (the shape stage, rescale 0.5).
+    bf16 storage runs the 16-bit vector statistics path with bf16 unpacking
+    (bar 8e-3 / cc: bf16 keeps 8 significant bits)."""
     _, offsets = workloads.config4()
     shape = (int(offsets[-1]), 32)
     x, pos, neg = _case(3300, shape, dtype)
@@ -87,7 +89,33 @@ def test_step_rescale_varlen_config4(dev, dtype):
     xp, x0 = ops.flow_euler_step(to_dev(x, dev, dtype), to_dev(pos, dev, dtype), t, tp, SM,
                                  v_neg=to_dev(neg, dev, dtype), guidance_strength=5.0, guidance_rescale=0.5,
                                  seg_offsets=offsets)
-    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 8e-3}[dtype]
+    cc = float(np.float32(SM + (1 - SM) * t))
+    assert max_err(xp, storage_round(orc.flow_step(x, pred, t, tp), dtype)) <= tol / cc
+    assert max_err(x0, storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shift", [0, 1])
+def test_step_rescale_varlen_unaligned(dev, dtype, shift):
+    """Varlen rescale on the scalar path: shape (300, 3) with segments
+    [0, 121, 300], whose element bounds (363, 900) are not whole 16-byte
+    vectors, and the same state one element into its buffers (no 16-byte
+    alignment at all): the per-segment statistics blocks and the
+    elementwise pass then run their scalar loops."""
+    shape = (300, 3)
+    segs = np.array([0, 121, 300], np.int64)
+    x, pos, neg = _case(3800, shape, dtype)
+    t, tp = 0.77, 0.69
+    pred = orc.flow_rescale(x, orc.flow_cfg(pos, neg, 4.0), pos, t, SM, 0.6, segs)
+    bufs = []
+    for a in (x, pos, neg):
+        b = torch.zeros(a.size + shift, dtype=dtype, device=dev)
+        b[shift:] = to_dev(a.reshape(-1), dev, dtype)
+        bufs.append(b[shift:].reshape(shape))
+    xp, x0 = ops.flow_euler_step(bufs[0], bufs[1], t, tp, SM, v_neg=bufs[2], guidance_strength=4.0,
+                                 guidance_rescale=0.6, seg_offsets=segs)
+    tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 8e-3}[dtype]
     cc = float(np.float32(SM + (1 - SM) * t))
     assert max_err(xp, storage_round(orc.flow_step(x, pred, t, tp), dtype)) <= tol / cc
     assert max_err(x0, storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
@@ -97,7 +125,8 @@ def test_step_rescale_varlen_config4(dev, dtype):
 def test_step_rescale_config5_latent(dev, dtype):
     """The config-5 token rows (T = 201,436) x 32 latent channels as one
     varlen segment (6.4M elements: the statistics pass caps a segment at 256
-    blocks, so each block strides over two 16K-element chunks), and the same
+    blocks, so each block takes a share of ~25K elements in two load
+    groups), and the same
     state split into three segments of unequal sizes; two calls give the
     same bits (fixed-order sums).
 
@@ -136,9 +165,10 @@ def test_step_rescale_config5_latent(dev, dtype):
 
 
 def test_step_odd_rows_and_unaligned_state(dev):
-    """Rows of 12,289 elements (one statistics block per row; three
-    4,096-element elementwise blocks and a 1-element tail block per row; rows
-    starting at odd element offsets, so the scalar path runs), and
+    """Rows of 12,289 elements (one statistics block per row, one per
+    16,384 elements started; six 2,048-element elementwise blocks and a
+    1-element tail block per row; rows starting at odd element offsets, so
+    the scalar path runs), and
     the same state viewed one element into its buffer (no 16-byte
     alignment): the oracle's bits without rescale and its tolerance with it."""
     shape = (3, 12289)

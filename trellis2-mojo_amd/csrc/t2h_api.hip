@@ -435,12 +435,12 @@ int32_t t2h_qkv_linear_pack(const void* x, int64_t ldx, const void* w, int64_t r
     const char* fn = "t2h_qkv_linear_pack";
     if (dtype != T2H_F16 && dtype != T2H_BF16) return fail(T2H_EINVAL, "%s: operands must be f16 or bf16", fn);
     if (rows < 0 || heads <= 0 || heads > 65535 || in_features <= 0) return fail(T2H_EINVAL, "%s: bad shape", fn);
-    if (head_dim != gemm_head_dim())
-        return fail(T2H_EUNSUPPORTED, "%s: head_dim must be %d", fn, gemm_head_dim());
+    if (!gemm_head_dim_ok(head_dim)) return fail(T2H_EUNSUPPORTED, "%s: head_dim must be 64 or 128", fn);
     const int64_t n = 3 * (int64_t)heads * head_dim;
-    if (n % gemm_feature_tile() != 0 || n > INT32_MAX)
-        return fail(T2H_EUNSUPPORTED, "%s: 3 * heads * head_dim must be a multiple of %d (even heads)", fn,
-                    gemm_feature_tile());
+    // whole feature tiles, each wave's 128 features inside one tensor
+    if (n % gemm_feature_tile() != 0 || ((int64_t)heads * head_dim) % 128 != 0 || n > INT32_MAX)
+        return fail(T2H_EUNSUPPORTED, "%s: 3 * heads * head_dim must be a multiple of %d (heads: even for "
+                    "head_dim 128, a multiple of 4 for 64)", fn, gemm_feature_tile());
     if (in_features % gemm_k_step() != 0)
         return fail(T2H_EINVAL, "%s: in_features %d is not a multiple of %d", fn, in_features, gemm_k_step());
     if (ldx < in_features || ldx % 8 != 0) return fail(T2H_EINVAL, "%s: ldx must be >= in_features and a multiple of 8", fn);
@@ -708,7 +708,7 @@ int32_t t2h_modulation_add(const float* mod, const float* modulation, float* m, 
 // Flow-matching Euler step. The rescale's workspace holds the statistics
 // pass's f64 partial quads [nstats][4]: at most kStatsMaxPerSeg per segment.
 static int64_t stats_blocks(int64_t m) {
-    const int64_t c = (m + kStatsChunk - 1) / kStatsChunk;
+    const int64_t c = (m + kStatsMinShare - 1) / kStatsMinShare;
     return c < kStatsMaxPerSeg ? c : kStatsMaxPerSeg;
 }
 
@@ -718,7 +718,7 @@ int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size, int32_t n_seg_o
     if (n_seg_offsets > 0) {   // segment sizes unknown here: the largest total over any split
         const int64_t nseg = n_seg_offsets - 1;
         const int64_t a = nseg * (int64_t)kStatsMaxPerSeg;
-        const int64_t b = (rows * row_size + kStatsChunk - 1) / kStatsChunk + nseg;
+        const int64_t b = (rows * row_size + kStatsMinShare - 1) / kStatsMinShare + nseg;
         blocks = a < b ? a : b;
     } else {
         blocks = rows * stats_blocks(row_size);

@@ -1,6 +1,7 @@
 // The qkv linear fused with the self-attention epilogue and the head-major
 // pack (t2h_qkv_linear_pack), on the GEMM core (tiling and pipeline:
-// t2h_gemm_core.h): a wave's 128 features are one head. T2H_QKV_WAVES picks
+// t2h_gemm_core.h): a wave's 128 features are one head of 128 or two heads of
+// 64. T2H_QKV_WAVES picks
 // the layout: 8 (shipped; 64 tokens per wave, 128 accumulators, 10 % faster
 // on the config-5 qkv) or 4 (128 tokens per wave, direct-to-LDS loads).
 //
@@ -17,21 +18,24 @@ namespace t2h {
 namespace {
 
 // ---- qkv linear + attention epilogue + head-major pack ----------------------
-// The qkv GEMM's output [rows, 3, H, 128] never reaches memory. A wave's 128
-// features are one head (q, k or v: head hg = n / 128, tensor hg / H, head
-// hg % H) for kWT tokens (64 with 8 waves, 128 with 4), and each token's
-// head lives in two lanes (l and l ^ 32, 64 values each). Per token, in the
+// The qkv GEMM's output [rows, 3, H, HD] never reaches memory. A wave's 128
+// features are one head of HD = 128 or two heads of HD = 64 (q, k or v: head
+// hg = n / HD, tensor hg / H, head hg % H) for kWT tokens (64 with 8 waves,
+// 128 with 4), and each token's head lives in two lanes (l and l ^ 32, 64 or
+// 32 values each: the MFMA tile of feature tile fi holds features fi*32 +
+// 8q + 4h + i in lane half h). Per token, in the
 // order of the separate kernels
 // (bias_rms_rope_qkv, pack_q_z, pack_kv_z): + bias; q/k: RMS over the head,
 // x * rsqrt(sum x^2) * (gamma * sqrt(D)); q/k: RoPE on the in-lane pairs
 // (2p, 2p + 1) with cos/sin from the phase table or from the token's
 // position; q: * 1/sqrt(D); tokens >= rows: 0. The head then goes through
 // the wave's own LDS region (kStaged tokens at a time: 64 with 4 waves, 32
-// with 8, 16 KB or 8 KB) as 256-byte token rows and leaves as 16-byte
-// vectors: whole token rows (qh [H, mp, D], k [H, lp, D], vh [H, lp, D]) or,
-// for the transposed k [H, D, lp], 8 tokens of one feature gathered from 8
-// rows. Tiles past the last token row skip the GEMM and write the pads.
-constexpr int kHead = 128;
+// with 8, 16 KB or 8 KB) as 256-byte token rows (one or two heads) and
+// leaves as 16-byte vectors: whole token rows of each head (qh [H, mp, D],
+// k [H, lp, D], vh [H, lp, D]) or, for the transposed k [H, D, lp], 8 tokens
+// of one feature gathered from 8 rows. Tiles past the last token row skip the
+// GEMM and write the pads.
+constexpr int kHead = 128;   // features of a wave (one staged token row: 256 bytes of 16-bit values)
 static_assert(kTJ == 2 || kTJ == 4, "copy_col cases");
 constexpr int kStaged = kWaves == 8 ? 32 : 64;   // token rows a wave stages at a time
 constexpr int kJJ = kStaged / 32;                // token tiles per staged group
@@ -57,14 +61,18 @@ __device__ __forceinline__ void copy_col(const f32x16 (&acc)[kFI][kTJ], float (&
         for (int r = 0; r < 16; ++r) col[fi][r] = acc[fi][TJ][r];
 }
 
-template <typename T, bool KT>
+template <typename T, bool KT, int HD>
 __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(GemmArgs g, PackArgs p, RopeSlots tab) {
+    constexpr int NH = kHead / HD;    // heads per wave
+    constexpr int FPH = kFI / NH;     // 32-feature MFMA tiles per head
+    constexpr int CPH = HD / 8;       // 16-byte chunks of a head's token row
     // One LDS array: the GEMM's stages, then the epilogue's staging (a
     // region per wave) and the tile's parameters at 64 KB. (A separate
     // parameter array that took the kernel past 128 KB of LDS measured 20 %
     // slower on MI355X.)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * kStageBytes];
-    static_assert(kWF == kHead && kWT % kStaged == 0 && kParamOff + 2 * 2 * kHead * 4 <= kStages * kStageBytes,
+    static_assert(kWF == kHead && kHead % HD == 0 && kFI % NH == 0 && kWT % kStaged == 0 &&
+                      kParamOff + 2 * 2 * kHead * 4 <= kStages * kStageBytes,
                   "staging layout");
     static_assert(kPPT * kGemmThreads == 2 * 2 * kHead, "parameters per thread");
     TileOf tile;
@@ -75,23 +83,27 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int wf = wave & 1, wt = wave >> 1;
     const int fr = lane & 31, h = lane >> 5;
-    const int hg = (int)((n0 + wf * kWF) / kHead);
-    const int which = hg / p.heads;          // 0 q, 1 k, 2 v (the block's two heads share it)
-    const int z = hg - which * p.heads;
+    const int hg = (int)((n0 + wf * kWF) / HD);
+    const int which = hg / p.heads;          // 0 q, 1 k, 2 v (the wave's heads share it: 128 | H * HD)
+    const int z = hg - which * p.heads;      // the wave's first head
     const float* __restrict__ bias = which == 0 ? p.bias_q : which == 1 ? p.bias_k : p.bias_v;
     const float* __restrict__ gamma = which == 0 ? p.gamma_q : which == 1 ? p.gamma_k : nullptr;
 
-    // the tile's bias and gamma * sqrt(D) (slot i = (head * 2 + kind) * 128 +
-    // d, kPPT slots per thread) are requested before the GEMM and land in LDS
-    // after it
+    // the tile's bias and gamma * sqrt(D) (slot i = (wave group * 2 + kind) *
+    // 128 + d, kPPT slots per thread; a group's 128 features are consecutive
+    // in the [H * HD] parameter rows) are requested before the GEMM and land
+    // in LDS after it
     float pv[kPPT];
 #pragma unroll
     for (int j = 0; j < kPPT; ++j) {
         const int i = (int)threadIdx.x + j * kGemmThreads;
         const int ph = i / (2 * kHead), kind = (i / kHead) & 1, pd = i % kHead;
-        const int pz = (int)((n0 + ph * kWF) / kHead) - which * p.heads;
-        const float* src = kind == 0 ? bias : gamma;
-        pv[j] = src != nullptr ? src[pz * kHead + pd] : 0.0f;
+        const int hp = (int)((n0 + ph * kWF) / HD);
+        const int wp = hp / p.heads;
+        const int pz = hp - wp * p.heads;
+        const float* src = kind == 0 ? (wp == 0 ? p.bias_q : wp == 1 ? p.bias_k : p.bias_v)
+                                     : (wp == 0 ? p.gamma_q : wp == 1 ? p.gamma_k : nullptr);
+        pv[j] = src != nullptr ? src[pz * HD + pd] : 0.0f;
     }
     f32x16 acc[kFI][kTJ];
     zero_acc(acc);
@@ -136,11 +148,11 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
             float cs[kFI][4][4];
             const bool table = rope && p.phases != nullptr;
             if (table) {
-                const float* row = p.phases + (tc % p.phase_rows) * kHead;
+                const float* row = p.phases + (tc % p.phase_rows) * HD;
 #pragma unroll
                 for (int fi = 0; fi < kFI; ++fi)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) load_params<4>(row + fi * 32 + q * 8 + h * 4, cs[fi][q]);
+                    for (int q = 0; q < 4; ++q) load_params<4>(row + (fi % FPH) * 32 + q * 8 + h * 4, cs[fi][q]);
             }
             if (bias != nullptr) {
 #pragma unroll
@@ -154,14 +166,19 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                         col[fi][q * 4 + 3] = add_rn(col[fi][q * 4 + 3], b4.w);
                     }
             }
-            // the head's sum of squares: 64 values here, 64 in lane ^ 32
-            float rn = 1.0f;
-            if (gamma != nullptr) {
-                float ss = 0.0f;
+            // each head's sum of squares: HD / 2 values here, HD / 2 in lane ^ 32
+            float rn[NH];
 #pragma unroll
-                for (int fi = 0; fi < kFI; ++fi) ss += sum_sq<16>(col[fi]);
-                ss += __shfl_xor(ss, 32);
-                rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+            for (int hh = 0; hh < NH; ++hh) rn[hh] = 1.0f;
+            if (gamma != nullptr) {
+#pragma unroll
+                for (int hh = 0; hh < NH; ++hh) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int fi = hh * FPH; fi < (hh + 1) * FPH; ++fi) ss += sum_sq<16>(col[fi]);
+                    ss += __shfl_xor(ss, 32);
+                    rn[hh] = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
+                }
             }
             float pos[T2H_MAX_POS_DIM];
             if (rope && !table) {
@@ -175,10 +192,11 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const float4 g4 = *reinterpret_cast<const float4*>(pg + fi * 32 + q * 8 + h * 4);
-                        v[q * 4 + 0] = (v[q * 4 + 0] * rn) * g4.x;
-                        v[q * 4 + 1] = (v[q * 4 + 1] * rn) * g4.y;
-                        v[q * 4 + 2] = (v[q * 4 + 2] * rn) * g4.z;
-                        v[q * 4 + 3] = (v[q * 4 + 3] * rn) * g4.w;
+                        const float r = rn[fi / FPH];
+                        v[q * 4 + 0] = (v[q * 4 + 0] * r) * g4.x;
+                        v[q * 4 + 1] = (v[q * 4 + 1] * r) * g4.y;
+                        v[q * 4 + 2] = (v[q * 4 + 2] * r) * g4.z;
+                        v[q * 4 + 3] = (v[q * 4 + 3] * r) * g4.w;
                     }
                 }
                 if (rope) {
@@ -193,7 +211,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                         for (int q = 0; q < 4; ++q)
 #pragma unroll
                             for (int j = 0; j < 2; ++j) {
-                                const int sl = (fi * 32 + q * 8 + h * 4) / 2 + j;
+                                const int sl = ((fi % FPH) * 32 + q * 8 + h * 4) / 2 + j;
                                 float c, sn;
                                 slot_phase(pos, tab.axis[sl], tab.freq[sl], c, sn);
                                 rotate_pair(v[q * 4 + 2 * j], v[q * 4 + 2 * j + 1], c, sn);
@@ -225,7 +243,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                 const int c = lane & 15;
                 const u32x4 w = *reinterpret_cast<const u32x4*>(region + row * 256 + ((c ^ stage_swz(row)) * 16));
                 const int64_t t = tw + row;
-                if (t < extent) out_store16(out + ((int64_t)z * extent + t) * kHead + c * 8, w);
+                if (t < extent) out_store16(out + ((int64_t)(z + c / CPH) * extent + t) * HD + (c % CPH) * 8, w);
             }
         } else {
             // feature rows of the transposed k: lane (d, g) gathers feature d
@@ -254,7 +272,7 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
                     w.y = wv[1];
                     w.z = wv[2];
                     w.w = wv[3];
-                    out_store16(out + ((int64_t)z * kHead + d) * p.lp + t, w);
+                    out_store16(out + ((int64_t)z * HD + d) * p.lp + t, w);
                 }
             }
         }
@@ -263,17 +281,17 @@ __global__ __launch_bounds__(kGemmThreads, T2H_GEMM_OCC) void qkv_pack_kernel(Ge
     }
 }
 
-template <typename T>
+template <typename T, int HD>
 hipError_t qkv_typed(const GemmArgs& g, const PackArgs& p, const RopeSlots& tab, hipStream_t s) {
     const dim3 grid = grid_1d(g.nblocks), blk(kGemmThreads);
-    if (p.k_transposed) hipLaunchKernelGGL((qkv_pack_kernel<T, true>), grid, blk, 0, s, g, p, tab);
-    else hipLaunchKernelGGL((qkv_pack_kernel<T, false>), grid, blk, 0, s, g, p, tab);
+    if (p.k_transposed) hipLaunchKernelGGL((qkv_pack_kernel<T, true, HD>), grid, blk, 0, s, g, p, tab);
+    else hipLaunchKernelGGL((qkv_pack_kernel<T, false, HD>), grid, blk, 0, s, g, p, tab);
     return hipGetLastError();
 }
 
 }  // namespace
 
-int32_t gemm_head_dim() { return kHead; }
+bool gemm_head_dim_ok(int32_t head_dim) { return head_dim == 128 || head_dim == 64; }
 
 hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, hipStream_t s) {
     // token tiles cover the pad rows of the outputs too (they are written as 0)
@@ -284,8 +302,12 @@ hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, 
     g.nblocks = ((span + kBT - 1) / kBT) * g.ftiles;
     g.tgroup = tile_group(g.k);
     if (g.nblocks == 0) return hipSuccess;
-    if (g.dtype == T2H_F16) return qkv_typed<_Float16>(g, p, tab, s);
-    return qkv_typed<__bf16>(g, p, tab, s);
+    if (p.head_dim == 64) {
+        if (g.dtype == T2H_F16) return qkv_typed<_Float16, 64>(g, p, tab, s);
+        return qkv_typed<__bf16, 64>(g, p, tab, s);
+    }
+    if (g.dtype == T2H_F16) return qkv_typed<_Float16, 128>(g, p, tab, s);
+    return qkv_typed<__bf16, 128>(g, p, tab, s);
 }
 
 }  // namespace t2h

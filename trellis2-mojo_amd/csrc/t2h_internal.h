@@ -75,6 +75,7 @@ struct QkArgs {
     int32_t coord_cols;
     int32_t grid_res;        // position source 3
     int64_t fper;            // logical tiles per front (set at launch)
+    int32_t cached;          // set at launch: a share of the row loads with the default cache policy
 };
 
 // Self-attention epilogue + head-major packing (t2h_attn_pack).
@@ -153,14 +154,24 @@ constexpr int kEulerChunk = T2H_EULER_CHUNK;   // elements per block of the elem
 #ifndef T2H_STATS_MAXSEG
 #define T2H_STATS_MAXSEG 256
 #endif
+#ifndef T2H_STATS_MINSHARE
+#define T2H_STATS_MINSHARE 16384
+#endif
 constexpr int kStatsBlock = T2H_STATS_BLOCK;   // threads per block of the rescale's statistics pass
-constexpr int kStatsPer = T2H_STATS_PER;  // elements per thread per statistics load group
-constexpr int kStatsChunk = kStatsBlock * kStatsPer;   // 16384 elements
+constexpr int kStatsPer = T2H_STATS_PER;  // elements per thread per tensor in one statistics load group
+constexpr int kStatsChunk = kStatsBlock * kStatsPer;   // elements of one load group of a block
 constexpr int kStatsMaxPerSeg = T2H_STATS_MAXSEG;   // statistics blocks (f64 partials) per segment, at most
+constexpr int kStatsMinShare = T2H_STATS_MINSHARE;  // a segment gets one statistics block per this many elements
 constexpr int kEulerMaxSeg = 64;          // varlen segments carried in the kernel arguments
-// statistics blocks the built-in scratch of t2h_flow_euler_step_noalloc holds
-// (64 segments at the per-segment cap; 16,384 f64 quads = 512 KB per GPU)
-constexpr int kEulerScratchPartials = 16384;
+// statistics blocks the built-in scratch of t2h_flow_euler_step_noalloc holds:
+// every split into kEulerMaxSeg segments at the per-segment cap
+// (16,384 f64 quads = 512 KB per GPU)
+constexpr int kEulerScratchPartials = kEulerMaxSeg * kStatsMaxPerSeg;
+// a block of the elementwise pass covers whole 16-byte vectors of every
+// storage type on every thread (8 elements of 16-bit storage)
+static_assert(kEulerChunk % (kEulerBlock * 8) == 0, "T2H_EULER_CHUNK: a multiple of 8 * kEulerBlock");
+static_assert(kStatsPer % 8 == 0, "T2H_STATS_PER: whole 16-byte vectors of every storage type");
+static_assert(kStatsBlock % 64 == 0 && kStatsBlock <= 1024, "T2H_STATS_BLOCK: whole waves, one block");
 struct EulerArgs {
     const void* x;
     const void* v_pos;
@@ -244,7 +255,7 @@ hipError_t launch_pack(const PackArgs& a, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_gemm(GemmArgs a, hipStream_t s);
 int32_t gemm_feature_tile();   // output features per block (out_features must be a multiple)
 int32_t gemm_k_step();         // k per stage (in_features must be a multiple)
-int32_t gemm_head_dim();       // head_dim of the fused qkv GEMM + pack
+bool gemm_head_dim_ok(int32_t head_dim);   // head_dim the fused qkv GEMM + pack takes (64, 128)
 hipError_t launch_qkv_pack(GemmArgs g, const PackArgs& p, const RopeSlots& tab, hipStream_t s);
 hipError_t launch_gemm_residual(GemmArgs a, hipStream_t s);
 // t2h_sampler.hip

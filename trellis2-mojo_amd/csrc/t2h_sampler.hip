@@ -15,17 +15,17 @@
 // caller's token segments (varlen state, biased std).
 //
 // The rescale takes two launches:
-// - euler_stats_kernel: at most kStatsMaxPerSeg blocks of 1024 threads per
-//   segment (one per 16K elements) take equal shares of it, load them with
-//   16-byte loads, sum
+// - euler_stats_kernel: one block of 1024 threads per 16,384 elements of a
+//   segment, at most kStatsMaxPerSeg, take equal shares of it, load them with
+//   16-byte loads (16 elements of each tensor per thread per load group), sum
 //   x0_pos, x0_pos^2, x0_cfg, x0_cfg^2 in f64 per thread, reduce through DPP
 //   row sums and one LDS combine, and write one f64 partial quad per block.
 //   Its loads are ordinary (cached), so the elementwise pass that re-reads
 //   the same 3 tensors right after finds them in the infinity cache when
 //   they fit.
 // - euler_apply_kernel: each block (2048 elements) first sums its segment's
-//   partials (at most 256 quads, one per thread, fixed order) into the
-//   segment's ratio,
+//   partials (at most kStatsMaxPerSeg quads, in a fixed order per thread)
+//   into the segment's ratio,
 //   with its own element loads already in flight, then runs the elementwise
 //   step. Every block of a segment sums the same partials in the same order,
 //   so all of them compute the same ratio bits, and the result is

@@ -312,7 +312,8 @@ def qkv_linear_pack(x, weight, heads: int, bias=None, gamma_q=None, gamma_k=None
     pack: x [rows, K] (float16/bfloat16, rows may be strided), weight
     [3*H*D, K] of x's dtype, bias [3*H*D] float32 (or None), gammas [H, D]
     float32 -> (qh [H, mp, D] scaled by 1/sqrt(D), k [H, D, lp] (k_transposed)
-    or [H, lp, D], vh [H, lp, D]); pads zero; mp/lp 0 = rows. D = 128."""
+    or [H, lp, D], vh [H, lp, D]); pads zero; mp/lp 0 = rows. D = 128 (H
+    even) or 64 (H a multiple of 4)."""
     _dev(x, "qkv_linear_pack")
     _dev(weight, "qkv_linear_pack")
     dt = _dtype(x, "qkv_linear_pack")
