@@ -587,7 +587,8 @@ def small_t_block(torch, dev, reps):
       LN1 + modulate -> qkv epilogue in place (bias, RMS q/k, RoPE from the
       grid) -> self join + norm2 (affine) -> cross join + LN3 + modulate ->
       GELU-tanh + bias on the MLP hidden -> gated MLP join.
-    Timed as eager launches and as one HIP-graph replay per block."""
+    Timed as eager launches, as HIP-graph replays of 30 blocks (a forward's
+    blocks in one graph; per-block time) and of one block."""
     from t2h import block, nn, ops
 
     T, C, H, D, F = 4096, 1536, 12, 128, 6144
@@ -630,26 +631,47 @@ def small_t_block(torch, dev, reps):
         torch.cuda.synchronize()
         return s0.elapsed_time(s1) / n
 
-    eager = gpu_time(step, reps)
-    graph = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=s):
+    def capture(nblocks):
+        """One HIP graph of nblocks consecutive blocks (the reference enqueues
+        every block of a forward before one barrier, sparse_structure_flow.mojo:
+        191-206): each hipGraphLaunch costs a gap of ~8 us before the next one
+        starts (kernel trace), which a whole forward in one graph pays once."""
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
             step()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph.replay()
-    replay = gpu_time(graph.replay, reps)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                for _ in range(nblocks):
+                    step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph.replay()
+        return graph
+
+    g1 = capture(1)
+    replay1 = gpu_time(g1.replay, reps)
+    del g1
+    # eager and the 30-block graph in interleaved windows of 30 blocks
+    # (medians of 7: single windows vary by ~3 % between runs)
+    nb = 30
+    gf = capture(nb)
+    ev, gr = [], []
+    for _ in range(7):
+        ev.append(gpu_time(step, nb))
+        gr.append(gpu_time(gf.replay, 1) / nb)
+    del gf
+    eager, replay = statistics.median(ev), statistics.median(gr)
     res = {"tokens": T, "launches": 6, "bytes": nbytes,
-           "eager_us": round(eager * 1e3, 2), "graph_us": round(replay * 1e3, 2),
+           "eager_us": round(eager * 1e3, 2), "graph_us": round(replay * 1e3, 2), "graph_blocks": nb,
+           "graph_1_block_us": round(replay1 * 1e3, 2),
            "eager_gbs": round(nbytes / eager / 1e6, 1), "graph_gbs": round(nbytes / replay / 1e6, 1),
+           "eager_pct_peak": round(nbytes / eager / 1e6 / HBM_PEAK_GBS * 100, 2),
            "graph_pct_peak": round(nbytes / replay / 1e6 / HBM_PEAK_GBS * 100, 2)}
     log(f"  ss-flow block glue + qk f32 [4096]: eager {eager*1e3:.1f} us ({nbytes/eager/1e6:.0f} GB/s), "
-        f"graph replay {replay*1e3:.1f} us ({nbytes/replay/1e6:.0f} GB/s)")
-    del graph
+        f"graph of {nb} blocks {replay*1e3:.1f} us/block ({nbytes/replay/1e6:.0f} GB/s), graph of one block "
+        f"{replay1*1e3:.1f} us")
     return res
 
 
@@ -730,6 +752,50 @@ def next_rows(torch, dev, chain, reps):
 
     rec_f("hipblaslt_fc2_then_gate_residual", hipblaslt_fc2_then_join, f2)
     del w2, hmid
+    return res
+
+
+def small_chain(torch, dev, tokens, steps):
+    """The config-5 chain (same ops, widths, f16) over one sparse batch of
+    `tokens` random voxels of the 128^3 grid: 2,369 is the structured-latent
+    DiT's token count in the reference's 512 pipeline. Launched eagerly back to
+    back (a GPU spin ahead lets the host enqueue every launch first) and as
+    one HIP graph of `steps` chain steps."""
+    ch = Chain(dev, torch.float16, tokens)
+    for _ in range(3):
+        ch.step()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(steps * 100_000)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(steps):
+        ch.step()
+    s1.record()
+    torch.cuda.synchronize()
+    eager = s0.elapsed_time(s1) / steps
+    graph = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ch.step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=st):
+            for _ in range(steps):
+                ch.step()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    graph.replay()
+    replay = time_region(torch, graph.replay, 3) / 3 / steps
+    del graph
+    res = {"tokens": tokens, "bytes": ch.chain_bytes}
+    for k, ms in (("eager", eager), ("graph", replay)):
+        gbs = ch.chain_bytes / ms / 1e6
+        res[k] = {"us_per_step": round(ms * 1e3, 2), "gbs": round(gbs, 1), "pct_of_peak": round(gbs / HBM_PEAK_GBS * 100, 2),
+                  "tokens_per_s": round(tokens / ms * 1e3)}
+        log(f"  T={tokens} {k}: {ms*1e3:.1f} us/step, {gbs:.1f} GB/s ({gbs/HBM_PEAK_GBS*100:.1f}%), "
+            f"{tokens/ms/1e3:.1f} M tokens/s")
+    del ch
+    torch.cuda.empty_cache()
     return res
 
 
@@ -893,6 +959,8 @@ def main():
     extra = next_rows(torch, dev, chain, max(10, args.steps))
     log("small-T block (dense sparse-structure DiT, 4096 tokens):")
     small = small_t_block(torch, dev, max(20, args.steps))
+    log("the chain at the SLat token count (one sparse batch of 2,369 tokens):")
+    slat = small_chain(torch, dev, 2369, max(200, args.steps))
     other = None
     if not args.no_configs:
         log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")
@@ -919,6 +987,7 @@ def main():
                                                                       "cpu_model")},
         "configs": other,
         "small_t_block": small,
+        "slat_chain": slat,
     }
     print(json.dumps(out), flush=True)
 

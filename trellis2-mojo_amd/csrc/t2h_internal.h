@@ -75,7 +75,6 @@ struct QkArgs {
     int32_t coord_cols;
     int32_t grid_res;        // position source 3
     int64_t fper;            // logical tiles per front (set at launch)
-    int32_t cached;          // set at launch: a share of the row loads with the default cache policy
 };
 
 // Self-attention epilogue + head-major packing (t2h_attn_pack).

@@ -38,15 +38,6 @@ constexpr int kWaves = kBlock / 64;
 #ifndef T2H_QK_WAVES
 #define T2H_QK_WAVES 8
 #endif
-#ifndef T2H_QK_ORDER
-#define T2H_QK_ORDER 0
-#endif
-#ifndef T2H_QK_CACHED
-#define T2H_QK_CACHED 0   // 1: one 1 KB piece of each 16-bit row with the default cache policy
-#endif
-#ifndef T2H_QK_CACHED_PIECE
-#define T2H_QK_CACHED_PIECE 0
-#endif
 constexpr int kTileWaves = T2H_QK_WAVES;   // token rows (one per wave) per tile block
 constexpr int kSmallTileWaves = 4;         // ... when the launch is short of rows (launch_fast)
 
@@ -68,14 +59,10 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     const int has_v = a.v != nullptr && a.bias_v != nullptr;
     const int upr = has_q + has_k + has_v;
     const int64_t b = block_linear();
-    // T2H_QK_ORDER 0: the tensors of a row tile in adjacent blocks; 1: every
-    // tile of q, then of k (then v)
-    const int64_t ntiles = (a.rows + W - 1) / W;
-    int which = T2H_QK_ORDER ? (int)(b / ntiles) : (int)(b % upr);   // 0 = q, 1 = k, 2 = v (absent skipped)
+    int which = (int)(b % upr);   // 0 = q, 1 = k, 2 = v (absent tensors skipped)
     if (!has_q) ++which;
     if (which == 1 && !has_k) ++which;
-    const int64_t tile = T2H_QK_ORDER ? b % ntiles : front_of(b / upr, a.fper);
-    if (T2H_QK_ORDER && b >= ntiles * upr) return;
+    const int64_t tile = front_of(b / upr, a.fper);
     if (tile * W >= a.rows) return;   // past the last tile of a 2-D grid (block-uniform)
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t r = tile * W + wave;
@@ -152,10 +139,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     for (int it = 0; it < NG; ++it) {
         const int hh = 4 * it + g;
         const int hl = hh < H ? hh : H - 1;
-        if (T2H_QK_CACHED && kEarly && L::NC == 1 && it == T2H_QK_CACHED_PIECE && a.cached)
-            load_elems_cached<T, E>(in + rl * a.in_stride, (int64_t)hl * D + m * E, (int64_t)H * D, v[it]);
-        else
-            L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
+        L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
     }
     if constexpr (kEarly) {
 #pragma unroll
@@ -342,8 +326,6 @@ hipError_t launch_fast(QkArgs a, const RopeSlots& tab, hipStream_t s) {
     const bool small = (a.rows + kTileWaves - 1) / kTileWaves * upr < 8LL * device_cu_count();
     const int w = small ? kSmallTileWaves : kTileWaves;
     const int64_t tiles = (a.rows + w - 1) / w;
-    a.cached = a.rows * (int64_t)a.heads * a.head_dim * (int64_t)sizeof(T) * 2 * upr >= T2H_CACHED_SHARE_MIN &&
-               (int64_t)a.heads * a.head_dim * (int64_t)sizeof(T) <= INT32_MAX;
     a.fper = front_per(tiles);
     const dim3 grid = grid_1d(front_grid(tiles) * upr);
     if (small) hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kSmallTileWaves>), grid, dim3(kSmallTileWaves * 64), 0, s, a, tab);
