@@ -53,6 +53,8 @@ def parse():
     p.add_argument("--op", default=None, help="time only one op of the chain (for profiling)")
     p.add_argument("--sweep", action="store_true",
                    help="time the config-5 chain at several token counts and print their JSON")
+    p.add_argument("--small-t", action="store_true",
+                   help="time only the small-T block and the chain at the SLat token count and print their JSON")
     return p.parse_args()
 
 
@@ -289,6 +291,11 @@ def steady_state(torch, chain, settle_ms, steps, rounds=3):
     order = [fns[n] for n in Chain.ORDER]
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(order) + 1)] for _ in range(steps)]
     torch.cuda.synchronize()
+    # ten untimed chain steps ahead of the window (~16 ms of GPU work): the
+    # host enqueues the window's launches and events meanwhile, so no
+    # interval waits for the host and the GPU never idles
+    for _ in range(10):
+        chain.step()
     for k in range(steps):
         e = ev[k]
         e[0].record()
@@ -875,6 +882,11 @@ def main():
     ops.device_init(0)
     if args.sweep:
         chain_sweep(torch, dev, args.steps)
+        return
+    if args.small_t:
+        small = small_t_block(torch, dev, max(20, args.steps))
+        slat = small_chain(torch, dev, 2369, max(200, args.steps))
+        print(json.dumps({"small_t_block": small, "slat_chain": slat}), flush=True)
         return
     if args.configs_only:
         log("BASELINE configs 1-4 (median of 30, warm / cold = caches flushed by a 1 GiB fill):")

@@ -237,7 +237,8 @@ int32_t t2h_linear_gate_residual(const void* x, int64_t ldx, const void* w,
  * x [rows, in_features] (rows ldx elements apart) and w [3*heads*head_dim,
  * in_features] (the qkv linear's [out, in] weight), both f16 or both bf16,
  * f32 sums. Biases, gammas, RoPE sources and outputs as t2h_attn_pack; all
- * three outputs are required. head_dim must be 128 and heads even;
+ * three outputs are required. head_dim 128 with heads even, or head_dim 64
+ * with heads a multiple of 4 (a wave's 128 features are one head or two);
  * in_features % 64 == 0. */
 int32_t t2h_qkv_linear_pack(const void* x, int64_t ldx, const void* w,
                             int64_t rows, int32_t in_features, int32_t heads,
