@@ -810,14 +810,26 @@ def chain_sweep(torch, dev, steps):
     """The config-5 chain (same ops, widths and f16 storage) at token counts
     from the dense sparse-structure grid (4,096) to 2.6x config 5, one batch
     of random voxels each: how the chain's HBM efficiency grows with T.
-    Prints one JSON line."""
+    GPU time of n back-to-back steps enqueued behind a GPU spin. Prints one
+    JSON line."""
     res = {}
     for tokens in (4096, 16384, 65536, 201436, 524288):
         ch = Chain(dev, torch.float16, tokens)
         for _ in range(3):
             ch.step()
-        n = max(5, min(steps, int(2e5 // tokens) * 10))
-        ms = time_region(torch, ch.step, n) / n
+        n = max(20, min(steps, int(2e5 // tokens) * 10))
+        # a GPU spin ahead of the window lets the host enqueue every launch
+        # first: at small T one Python call of an op takes longer than its
+        # kernel, and the window would time the host
+        torch.cuda.synchronize()
+        torch.cuda._sleep(n * 150_000)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(n):
+            ch.step()
+        s1.record()
+        torch.cuda.synchronize()
+        ms = s0.elapsed_time(s1) / n
         gbs = ch.chain_bytes / ms / 1e6
         res[str(tokens)] = {"us_per_step": round(ms * 1e3, 2), "gbs": round(gbs, 1),
                             "pct_peak": round(gbs / HBM_PEAK_GBS * 100, 2), "tokens_per_s": round(tokens / ms * 1e3)}

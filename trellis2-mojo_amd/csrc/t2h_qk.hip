@@ -121,17 +121,21 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     float cpos = 0.0f;
     if (live && coord_pos && my_axis >= 0) cpos = (float)a.coords[r * a.coord_cols + 1 + my_axis];
 
-    // gamma * scale and the bias, staged in LDS once per block
+    // gamma * scale and the bias, staged in LDS once per block. A thread
+    // holds at most two float4s of each in named registers: an array indexed
+    // by a loop counter is placed in LDS (or scratch) by the compiler before
+    // the loop is unrolled, and its store would wait for the parameter load
+    // ahead of the row loads
     constexpr int KP = (NG * D + W * 64 - 1) / (W * 64);   // parameter float4s per thread
+    static_assert(KP <= 2, "parameter float4s per thread");
     const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
-    float4 gl[KP], bl[KP];
+    const int pi0 = threadIdx.x, pi1 = threadIdx.x + W * 64;
+    float4 gl0 = make_float4(0.f, 0.f, 0.f, 0.f), gl1 = gl0, bl0 = gl0, bl1 = gl0;
     if constexpr (kEarly) {
-#pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            const int i = threadIdx.x + k * W * 64;
-            if (gamma != nullptr && i < HD / 4) gl[k] = reinterpret_cast<const float4*>(gamma)[i];
-            if (bias != nullptr && i < HD / 4) bl[k] = reinterpret_cast<const float4*>(bias)[i];
-        }
+        if (gamma != nullptr && pi0 < HD / 4) gl0 = reinterpret_cast<const float4*>(gamma)[pi0];
+        if (bias != nullptr && pi0 < HD / 4) bl0 = reinterpret_cast<const float4*>(bias)[pi0];
+        if (KP > 1 && gamma != nullptr && pi1 < HD / 4) gl1 = reinterpret_cast<const float4*>(gamma)[pi1];
+        if (KP > 1 && bias != nullptr && pi1 < HD / 4) bl1 = reinterpret_cast<const float4*>(bias)[pi1];
     }
     const int64_t rl = live ? r : a.rows - 1;   // dead waves load a valid row, store nothing
     float v[NG][E];
@@ -142,15 +146,13 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
     }
     if constexpr (kEarly) {
-#pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            const int i = threadIdx.x + k * W * 64;
-            if (gamma != nullptr && i < HD / 4) {
-                const float sc = a.rms_scale;
-                reinterpret_cast<float4*>(gs)[i] = make_float4(gl[k].x * sc, gl[k].y * sc, gl[k].z * sc, gl[k].w * sc);
-            }
-            if (bias != nullptr && i < HD / 4) reinterpret_cast<float4*>(bs)[i] = bl[k];
-        }
+        const float sc = a.rms_scale;
+        if (gamma != nullptr && pi0 < HD / 4)
+            reinterpret_cast<float4*>(gs)[pi0] = make_float4(gl0.x * sc, gl0.y * sc, gl0.z * sc, gl0.w * sc);
+        if (bias != nullptr && pi0 < HD / 4) reinterpret_cast<float4*>(bs)[pi0] = bl0;
+        if (KP > 1 && gamma != nullptr && pi1 < HD / 4)
+            reinterpret_cast<float4*>(gs)[pi1] = make_float4(gl1.x * sc, gl1.y * sc, gl1.z * sc, gl1.w * sc);
+        if (KP > 1 && bias != nullptr && pi1 < HD / 4) reinterpret_cast<float4*>(bs)[pi1] = bl1;
     } else {
         if (gamma != nullptr) {
             for (int i = threadIdx.x; i < HD; i += W * 64) gs[i] = gamma[i] * a.rms_scale;
