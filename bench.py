@@ -487,25 +487,29 @@ def other_configs(torch, dev, cpu=True):
         """Back-to-back launches over rotating buffer sets whose footprint
         (>= 600 MB) exceeds the 256 MB infinity cache: every launch reads
         HBM, and a launch's dispatch overlaps its predecessor's tail, as in
-        a block sequence."""
+        a block sequence. ~60 launches (the sets in turn) per event pair."""
         k = max(2, -(-600_000_000 // (2 * nbytes)))
         fns = [make() for _ in range(k)]
         for f in fns:
             f()
+        rounds = max(1, 60 // k)   # ~60 launches per window, so the two events' cost is spread thin
         times = []
         for _ in range(9):
             torch.cuda.synchronize()
-            torch.cuda._sleep(2_000_000)   # ~1 ms of GPU spin: the host enqueues all k launches meanwhile
+            # ~5 ms of GPU spin: the host enqueues all k * rounds launches meanwhile
+            torch.cuda._sleep(10_000_000)
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
-            for f in fns:
-                f()
+            for _ in range(rounds):
+                for f in fns:
+                    f()
             e.record()
             torch.cuda.synchronize()
             times.append(s.elapsed_time(e))
-        ms = statistics.median(times) / k
+        ms = statistics.median(times) / (k * rounds)
         res[name].update({"stream_us": round(ms * 1e3, 2), "stream_gbs": round(nbytes / ms / 1e6, 1),
-                          "stream_pct_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 2), "stream_sets": k})
+                          "stream_pct_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 2), "stream_sets": k,
+                          "stream_launches": k * rounds})
         log(f"  {name:<28s} back-to-back over {k} buffer sets: {ms*1e3:8.1f} us {nbytes/ms/1e6:8.1f} GB/s "
             f"({nbytes/ms/1e6/HBM_PEAK_GBS*100:5.1f}%)")
         del fns

@@ -38,8 +38,13 @@ namespace {
 #define T2H_PACK_ROWS 64
 #endif
 constexpr int kPackRows = T2H_PACK_ROWS;   // token rows per tile block
-constexpr int kPackBlock = 256;
-constexpr int kPackIters = kPackRows / 16;   // row groups of 4 per wave
+#ifndef T2H_PACK_WAVES
+#define T2H_PACK_WAVES 4
+#endif
+constexpr int kPackBlock = 64 * T2H_PACK_WAVES;
+constexpr int kPackRowsPerIter = 4 * T2H_PACK_WAVES;         // a wave instruction covers 4 rows
+constexpr int kPackIters = kPackRows / kPackRowsPerIter;    // row groups of 4 per wave
+static_assert(kPackIters * kPackRowsPerIter == kPackRows, "tile rows");
 
 // One lane's E elements of one head row, held as the loaded 32-bit words so
 // that a prefetch stays in flight until the words are unpacked.
@@ -114,7 +119,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
     int64_t rl[kPackIters];
 #pragma unroll
     for (int it = 0; it < kPackIters; ++it) {
-        const int64_t t = t0 + it * 16 + wave * 4 + g;
+        const int64_t t = t0 + it * kPackRowsPerIter + wave * 4 + g;
         rl[it] = t < a.rows ? t : (a.rows > 0 ? a.rows - 1 : 0);
     }
 
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
         }
 #pragma unroll
         for (int it = 0; it < kPackIters; ++it) {
-            const int64_t t = t0 + it * 16 + wave * 4 + g;
+            const int64_t t = t0 + it * kPackRowsPerIter + wave * 4 + g;
             float* x = v[it];
             if (bias != nullptr) {
 #pragma unroll
@@ -206,7 +211,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
                 for (int i = 0; i < E; ++i) x[i] = 0.0f;
             }
             if constexpr (KT) {
-                const int tl = it * 16 + wave * 4 + g;
+                const int tl = it * kPackRowsPerIter + wave * 4 + g;
 #pragma unroll
                 for (int i = 0; i < E; ++i) tile[tl][L::elem(m, i)] = round_to<T>(x[i]);
             } else if (t < extent) {
