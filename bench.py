@@ -7,8 +7,8 @@ sparse tokens (a thickened sphere shell on a 128^3 grid), width 1536,
 
     timestep embedding [1, 256]
     -> LayerNorm + adaLN modulate          x[T,1536] -> h[T,1536]
-    -> QK RMSNorm + 3D RoPE from coords    q,k[T,12,128] -> q',k'
-    -> GELU-tanh(+bias)                    u[T,6144] -> g[T,6144]
+    -> QK RMSNorm + 3D RoPE from coords    q,k[T,12,128], in place
+    -> GELU-tanh(+bias)                    u[T,6144], in place
     -> gated residual                      x + gate*y -> out[T,1536]
 
 One step = one pass of this chain; inputs are resident in HBM before the
@@ -92,13 +92,20 @@ class Chain:
             rn((1, C), 0.1, dt=torch.float32)
         self.h = torch.empty_like(self.x)
         self.q, self.k = rn((T, H, D)), rn((T, H, D))
-        self.qo, self.ko = torch.empty_like(self.q), torch.empty_like(self.k)
         self.gq, self.gk = rn((H, D), 0.02, 1.0, torch.float32), rn((H, D), 0.02, 1.0, torch.float32)
         self.freqs = nn.rope_freqs(D)
         self.u = rn((T, F))
         self.bias = rn((F,), 0.02, dt=torch.float32)
-        self.gout = torch.empty_like(self.u)
         self.y = rn((T, C))
+        # QK and GELU + bias run in place, as the reference's device kernels
+        # do (bias_rms_rope_qkv on the qkv rows, gpu/attention.mojo:507-563;
+        # gelu_tanh_bias on the fc1 rows, gpu/linear.mojo:662-690): the bytes
+        # of an out-of-place launch over half the pages, 2 % and 1 % faster.
+        # The gated residual writes a new tensor: in place on x (as
+        # gpu/block.mojo:86-110 does) the next step's LN + modulate ran
+        # 15-17 us slower, more than the residual gained.
+        self.qo, self.ko = self.q, self.k
+        self.gout = self.u
         self.res = torch.empty_like(self.x)
         self.temb = None
         e = 2 if dtype != torch.float32 else 4
@@ -127,7 +134,7 @@ class Chain:
             return lambda: o.activation(self.u, o.ACT_GELU_TANH, bias=self.bias, out=self.gout)
         if name == "gate_residual":
             return lambda: o.gate_residual(self.x, self.y, gate=self.gate, offsets=self.offsets, out=self.res)
-        if name == "copy":  # calibration: torch's vectorized elementwise kernel copying the GELU tensor (y = x * 1)
+        if name == "copy":  # calibration: torch's vectorized elementwise kernel over the GELU tensor (u *= 1)
             return lambda: self.torch.mul(self.u, 1.0, out=self.gout)
         if name == "chain":
             return self.step
@@ -152,7 +159,7 @@ class Chain:
     # so only the glue kernels run), the attention epilogue + head-major pack,
     # and the sampler step on the tokens' 32-channel f32 latent
     NEXT_OPS = ("block_glue_fused", "block_glue_unfused", "attn_pack_kt", "attn_pack_krows",
-                "flow_euler_step_cfg", "flow_euler_step_cfg_rescale")
+                "flow_euler_step_cfg", "flow_euler_step_cfg_rescale", "flow_euler_step_cfg_rescale_two_launch")
 
     def next_state(self):
         if getattr(self, "_next", None) is None:
@@ -172,6 +179,7 @@ class Chain:
             st["lat"] = [torch.randn((T, 32), generator=g, device=dev) for _ in range(3)]
             st["lat_out"] = [torch.empty((T, 32), device=dev) for _ in range(2)]
             st["ws"] = torch.empty(ops.flow_euler_workspace(T, 32, 2), dtype=torch.uint8, device=dev)
+            st["ws2"] = torch.empty(256 * 32, dtype=torch.uint8, device=dev)   # 256 statistics partials
             self._next = st
         return self._next
 
@@ -183,9 +191,12 @@ class Chain:
         return {"block_glue_fused": 13 * T * C * e, "block_glue_unfused": 15 * T * C * e,   # row-passes of C
                 "attn_pack_kt": T * 3 * C * e + 3 * mp * C * e + T * 16,
                 "attn_pack_krows": T * 3 * C * e + 3 * mp * C * e + T * 16,
-                # CFG: reads x, v_pos, v_neg, writes x_prev, pred_x0; the rescale's
-                # statistics pass reads the three inputs once more
-                "flow_euler_step_cfg": 5 * n, "flow_euler_step_cfg_rescale": 8 * n}[name]
+                # CFG: reads x, v_pos, v_neg, writes x_prev, pred_x0. The rescale in
+                # one launch holds the three inputs in registers across its grid
+                # barrier (the same five passes); in two launches its statistics
+                # pass reads them once more
+                "flow_euler_step_cfg": 5 * n, "flow_euler_step_cfg_rescale": 5 * n,
+                "flow_euler_step_cfg_rescale_two_launch": 8 * n}[name]
 
     def next_op(self, name):
         from t2h import block, ops
@@ -205,9 +216,11 @@ class Chain:
         if name == "flow_euler_step_cfg":
             return lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2], guidance_strength=3.0,
                                                x_prev=lo[0], pred_x0=True)
-        # CFG 3.0 + rescale 0.5 over one token segment
+        # CFG 3.0 + rescale 0.5 over one token segment; a workspace without
+        # room for the one-launch form's barrier gives the two-launch form
+        ws = st["ws"] if name == "flow_euler_step_cfg_rescale" else st["ws2"]
         return lambda: ops.flow_euler_step(lat[0], lat[1], 0.8, 0.7, 1e-5, v_neg=lat[2], guidance_strength=3.0,
-                                           guidance_rescale=0.5, seg_offsets=[0, self.T], workspace=st["ws"],
+                                           guidance_rescale=0.5, seg_offsets=[0, self.T], workspace=ws,
                                            x_prev=lo[0])
 
     # the GEMM rows (f16 operands on the matrix cores): flops per launch
@@ -597,7 +610,7 @@ def small_t_block(torch, dev, reps):
     outputs stubbed by resident tensors:
       LN1 + modulate -> qkv epilogue in place (bias, RMS q/k, RoPE from the
       grid) -> self join + norm2 (affine) -> cross join + LN3 + modulate ->
-      GELU-tanh + bias on the MLP hidden -> gated MLP join.
+      GELU-tanh + bias in place on the MLP hidden -> gated MLP join.
     Timed as eager launches, as HIP-graph replays of 30 blocks (a forward's
     blocks in one graph; per-block time) and of one block."""
     from t2h import block, nn, ops
@@ -611,7 +624,6 @@ def small_t_block(torch, dev, reps):
     x0 = rn((T, C))
     x, hs, hs2 = x0.clone(), torch.empty(T, C, device=dev), torch.empty(T, C, device=dev)
     qkv, h_self, h_cross, hid, h_mlp = rn((T, 3 * C)), rn((T, C)), rn((T, C)), rn((T, F)), rn((T, C))
-    hid_out = torch.empty_like(hid)
     qkv_bias, fbias = rn((3 * C,), 0.02), rn((F,), 0.02)
     gq, gk = rn((H, D), 0.02, 1.0), rn((H, D), 0.02, 1.0)
     freqs = nn.rope_freqs(D)
@@ -621,7 +633,7 @@ def small_t_block(torch, dev, reps):
         ops.qkv_bias_rmsnorm_rope(qkv, H, D, bias=qkv_bias, gamma_q=gq, gamma_k=gk, freqs=freqs, grid_res=16)
         ops.block_join_ln(x, h_self, hs2, bk, 2 * C, 1, 4 * C, 2)
         ops.block_join_ln(x, h_cross, hs, bk, 6 * C, 0, 8 * C, 1)
-        ops.activation(hid, ops.ACT_GELU_TANH, bias=fbias, out=hid_out)
+        ops.activation(hid, ops.ACT_GELU_TANH, bias=fbias, out=hid)   # in place (gpu/linear.mojo:662-690)
         ops.gate_add_bias_rows(x, h_mlp, bk, 10 * C, 1)
 
     e = 4

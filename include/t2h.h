@@ -342,9 +342,16 @@ int32_t t2h_gate_residual_ln_modulate(
  *   pred_x0 = fl(x_t * f32(1 - sigma_min)) - fl(pred * f32(sigma_min + (1 - sigma_min) t))
  *            (NULL = not written)
  * The elementwise results are bit-exact with the reference; the rescale's
- * std is summed in f64 (the reference sums serially in f32). The rescale
- * needs a device workspace of t2h_flow_euler_workspace() bytes (16-byte
- * aligned); calls that share a workspace must not overlap. */
+ * std is summed in f64 (the reference sums serially in f32), in a fixed
+ * order, so repeated calls give the same bits. The rescale needs a device
+ * workspace of t2h_flow_euler_workspace() bytes (16-byte aligned, any
+ * contents); calls that share a workspace must not overlap. With one
+ * segment (rows == 1 dense, or two seg offsets) on whole 16-byte vectors
+ * and a workspace of that size, a state that fits the registers of the
+ * resident grid (up to ~7M f32 elements on MI355X) is rescaled in one
+ * launch whose blocks meet at a grid barrier in the workspace; a smaller
+ * workspace (at least the statistics partials', as the error names) gives
+ * the two-launch form. */
 int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size,
                                  int32_t n_seg_offsets);
 int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos,
@@ -359,10 +366,11 @@ int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos,
 /* No counterpart in the reference: t2h_flow_euler_step for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Same arguments without the
- * workspace: the rescale's statistics go to a scratch array built into the
- * library, 512 KB per GPU (16,384 statistics blocks: every varlen split of
- * up to 64 segments, or up to 16,384 dense rows of <= 16,384 elements each;
- * larger dense states return T2H_EUNSUPPORTED). It allocates nothing, and
+ * workspace: the rescale's statistics (and the one-launch form's barrier)
+ * go to a scratch array built into the library, 512 KB per GPU (16,384
+ * statistics blocks: every varlen split of up to 64 segments, or up to
+ * 16,384 dense rows of <= 16,384 elements each; larger dense states return
+ * T2H_EUNSUPPORTED). It allocates nothing, and
  * its results equal t2h_flow_euler_step's bit for bit. Every call on a GPU
  * shares that GPU's scratch, so calls that overlap on one GPU (other
  * streams, other threads) race; stream-ordered calls do not. Call

@@ -8,7 +8,9 @@ the coords, t * 1000 into the timestep embedding (samplers/flow_euler.mojo:
 -> QK RMSNorm + RoPE from the int coords -> GELU-tanh + bias -> gathered
 gated residual (sparse/transformer/modulated.mojo:60-65, 214-226;
 sparse/attention/rope.mojo:48-66; modules/nn.mojo:314-369, 588-647;
-models/sparse_structure_flow.mojo:60-76).
+models/sparse_structure_flow.mojo:60-76). QK and GELU run in place, as the
+reference's device kernels do; the fixture keeps a copy of each input from
+before the step.
 
 Every op is checked against the C oracle on sampled rows: the first and
 last 8-row tiles, a middle tile, 6 more whole 8-row tiles, the rows with
@@ -33,6 +35,8 @@ def chain(dev):
     import bench
 
     ch = bench.Chain(dev, torch.float16)
+    assert ch.qo.data_ptr() == ch.q.data_ptr() and ch.gout.data_ptr() == ch.u.data_ptr()
+    ch.x_in, ch.q_in, ch.k_in, ch.u_in = (t.clone() for t in (ch.x, ch.q, ch.k, ch.u))
     ch.temb = ch.op("timestep")()
     ch.step()
     torch.cuda.synchronize()
@@ -72,7 +76,7 @@ def test_config5_timestep(chain):
 
 def test_config5_ln_modulate_sampled_rows(chain):
     idx = _sample_rows(chain.coords_np)
-    x = host(chain.x[idx])
+    x = host(chain.x_in[idx])
     want = orc.ln_modulate(x, host(chain.shift), host(chain.scale), eps=1e-6)
     assert_close(chain.h[idx], want, torch.float16, "config-5 LN + gathered modulate")
 
@@ -80,7 +84,7 @@ def test_config5_ln_modulate_sampled_rows(chain):
 def test_config5_qk_rms_rope_sampled_rows(chain):
     idx = _sample_rows(chain.coords_np)
     ph = orc.rope_phases_from_coords(chain.coords_np[idx], chain.D, orc.rope_freqs(chain.D))
-    wq, wk = orc.qk_rms_rope(host(chain.q[idx]), host(chain.k[idx]), host(chain.gq), host(chain.gk), ph)
+    wq, wk = orc.qk_rms_rope(host(chain.q_in[idx]), host(chain.k_in[idx]), host(chain.gq), host(chain.gk), ph)
     assert_close(chain.qo[idx], wq, torch.float16, "config-5 q RMS + RoPE")
     assert_close(chain.ko[idx], wk, torch.float16, "config-5 k RMS + RoPE")
 
@@ -91,7 +95,7 @@ def test_config5_rope_keeps_pair_norms(chain):
     from t2h import ops
 
     T, H, D = chain.T, chain.H, chain.D
-    for src, gamma, out in ((chain.q, chain.gq, chain.qo), (chain.k, chain.gk, chain.ko)):
+    for src, gamma, out in ((chain.q_in, chain.gq, chain.qo), (chain.k_in, chain.gk, chain.ko)):
         rms = torch.empty_like(src)
         ops.qk_rmsnorm_rope(q=src, gamma_q=gamma, use_rope=False, q_out=rms)
         n_rope = out.float().reshape(T, H, D // 2, 2).square().sum(-1).sqrt()
@@ -103,7 +107,7 @@ def test_config5_rope_keeps_pair_norms(chain):
 
 def test_config5_gelu_sampled_rows(chain):
     idx = _sample_rows(chain.coords_np)
-    want = orc.gelu_tanh_bias(host(chain.u[idx]), host(chain.bias))
+    want = orc.gelu_tanh_bias(host(chain.u_in[idx]), host(chain.bias))
     assert_close(chain.gout[idx], want, torch.float16, "config-5 GELU-tanh + bias")
 
 
@@ -112,14 +116,14 @@ def test_config5_gated_residual(chain):
     x + fl(y * gate) in f32 (two separate single-rounding torch ops, the
     oracle's sequence) rounded once to f16."""
     idx = _sample_rows(chain.coords_np)
-    want = orc.gate_residual(host(chain.x[idx]), host(chain.y[idx]), host(chain.gate),
+    want = orc.gate_residual(host(chain.x_in[idx]), host(chain.y[idx]), host(chain.gate),
                              offsets=np.array([0, len(idx)], np.int64))
     assert bits_equal(chain.res[idx], storage_round(want, torch.float16), torch.float16)
     T = chain.T
     for lo in range(0, T, 65536):
         hi = min(T, lo + 65536)
         prod = torch.mul(chain.y[lo:hi].float(), chain.gate)
-        full = torch.add(chain.x[lo:hi].float(), prod).half()
+        full = torch.add(chain.x_in[lo:hi].float(), prod).half()
         assert torch.equal(chain.res[lo:hi].view(torch.int16), full.view(torch.int16)), f"rows {lo}:{hi}"
 
 
@@ -127,8 +131,8 @@ def test_config5_max_err_report(chain):
     """The largest per-op error on the sampled rows stays inside the f16
     tolerance with margin (printed for the record)."""
     idx = _sample_rows(chain.coords_np)
-    x = host(chain.x[idx])
+    x = host(chain.x_in[idx])
     e_ln = max_err(chain.h[idx], orc.ln_modulate(x, host(chain.shift), host(chain.scale), eps=1e-6))
-    e_ge = max_err(chain.gout[idx], orc.gelu_tanh_bias(host(chain.u[idx]), host(chain.bias)))
+    e_ge = max_err(chain.gout[idx], orc.gelu_tanh_bias(host(chain.u_in[idx]), host(chain.bias)))
     print(f"config-5 max err: LN+mod {e_ln:.2e}, GELU {e_ge:.2e} (f16 tol 2e-3)", flush=True)
     assert max(e_ln, e_ge) <= 2e-3

@@ -164,6 +164,103 @@ def test_step_rescale_config5_latent(dev, dtype):
             assert abs(x0d[lo:hi].std() / x0p[lo:hi].astype(np.float64).std() - 1) < 2e-6
 
 
+# the workspace of the one-launch rescale: the barrier words (a 64-bit error
+# word in the first 64 bytes, 8 release slots of 128 bytes each starting with
+# a 64-bit epoch, one 64-bit arrival flag per block for up to 4096 blocks),
+# then one f64 quad per block
+FUSE_BYTES = 64 + 8 * 128 + 4096 * 8 + 4096 * 32
+
+
+def _step(x, p, n, t, tp, g, gr, segs, ws):
+    return ops.flow_euler_step(x, p, t, tp, SM, v_neg=n, guidance_strength=g, guidance_rescale=gr,
+                               seg_offsets=segs, workspace=ws)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape,segs", [
+    ((201436, 32), [0, 201436]),      # the config-5 latent: one segment, 4 vectors per thread (f32)
+    ((4097, 32), [0, 4097]),          # a last block with 8 of its vectors
+    ((4097, 32), [5, 3000]),          # one segment with uncovered rows on both sides
+    ((3, 8), [0, 3]),                 # 24 elements: one partial block
+    ((1, 8 * 16 ** 3), None),         # a dense state of one row: unbiased std
+])
+def test_step_rescale_one_launch(dev, dtype, shape, segs):
+    """A single segment on whole 16-byte vectors takes the one-launch form
+    (inputs held in registers across a grid barrier). Against the oracle to
+    the sampler bars, and against the two-launch form (a workspace without
+    room for the barrier) to 2 ulp of the storage type: both sum the std in
+    f64, in different orders."""
+    rows = shape[0]
+    assert ops.flow_euler_workspace(rows, shape[1], 0 if segs is None else len(segs)) == FUSE_BYTES
+    x, pos, neg = _case(3900 + rows, shape, dtype)
+    t, tp, g, gr = 0.8, 0.72, 3.0, 0.6
+    so = None if segs is None else np.array(segs, np.int64)
+    pred = orc.flow_rescale(x, orc.flow_cfg(pos, neg, g), pos, t, SM, gr, so)
+    dx, dp, dn = (to_dev(a, dev, dtype) for a in (x, pos, neg))
+    one = _step(dx, dp, dn, t, tp, g, gr, segs, torch.empty(FUSE_BYTES, dtype=torch.uint8, device=dev))
+    two = _step(dx, dp, dn, t, tp, g, gr, segs, torch.empty(FUSE_BYTES - 16, dtype=torch.uint8, device=dev))
+    cc = float(np.float32(SM + (1 - SM) * t))
+    tol = {torch.float32: 3e-5, torch.float16: 2e-3, torch.bfloat16: 8e-3}[dtype]
+    assert max_err(one[0], storage_round(orc.flow_step(x, pred, t, tp), dtype)) <= tol / cc
+    assert max_err(one[1], storage_round(orc.flow_v_to_xstart(x, pred, t, SM), dtype)) <= tol / cc
+    ulp = {torch.float32: 2.0 ** -23, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[dtype]
+    for a, b in zip(one, two):
+        d = (a.float() - b.float()).abs() / b.float().abs().clamp(min=1.0)
+        assert d.max().item() <= 2 * ulp / cc, (shape, segs, d.max().item())
+    if segs is not None and segs[0] > 0:   # uncovered rows: x_prev = x exactly
+        assert torch.equal(one[0][:segs[0]], dx[:segs[0]]) and torch.equal(one[0][segs[1]:], dx[segs[1]:])
+
+
+def test_step_rescale_one_launch_repeats_on_a_dirty_workspace(dev):
+    """The barrier words need no set-up by the caller: on a workspace filled
+    with 0xFF bytes, three calls in a row give the same bits; each advances
+    every release slot's epoch by one and leaves the error word unequal to
+    it (a block that stopped waiting writes the new epoch there)."""
+    T = 201436
+    x, pos, neg = (to_dev(a, dev) for a in _case(4100, (T, 32)))
+    ws = torch.full((FUSE_BYTES,), 255, dtype=torch.uint8, device=dev)
+    outs = []
+    for call in range(3):
+        outs.append(_step(x, pos, neg, 0.8, 0.72, 3.0, 0.6, [0, T], ws))
+        words = ws[:64 + 8 * 128].view(torch.int64).cpu()
+        epochs = [int(words[8 + 16 * k]) for k in range(8)]
+        assert epochs == [call] * 8, epochs        # 0xFF..FF + 1 wraps to 0
+        assert int(words[0]) != epochs[0], "error word"
+    for o in outs[1:]:
+        assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
+
+
+def test_step_rescale_one_launch_in_a_hip_graph(dev):
+    """The one-launch step (its barrier reset and its grid) recorded into a
+    HIP graph: three replays with fresh inputs, eager steps on the same
+    workspace in between, each replay equal to an eager step bit for bit."""
+    T = 201436
+    x, pos, neg = (to_dev(a, dev) for a in _case(4200, (T, 32)))
+    ws = torch.empty(FUSE_BYTES, dtype=torch.uint8, device=dev)
+    xp, x0 = torch.empty_like(x), torch.empty_like(x)
+
+    def step():
+        return ops.flow_euler_step(x, pos, 0.8, 0.72, SM, v_neg=neg, guidance_strength=3.0, guidance_rescale=0.6,
+                                   seg_offsets=[0, T], workspace=ws, x_prev=xp)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _, gx0 = step()
+    g = torch.Generator(device=dev).manual_seed(4201)
+    for rep in range(3):
+        for a in (x, pos, neg):
+            a.copy_(torch.randn(a.shape, generator=g, device=dev))
+        graph.replay()
+        got = (xp.clone(), gx0.clone())
+        want = _step(x, pos, neg, 0.8, 0.72, 3.0, 0.6, [0, T], ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1]), f"replay {rep}"
+
+
 def test_step_odd_rows_and_unaligned_state(dev):
     """Rows of 12,289 elements (one statistics block per row, one per
     16,384 elements started; six 2,048-element elementwise blocks and a

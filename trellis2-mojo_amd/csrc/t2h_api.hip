@@ -723,7 +723,9 @@ int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size, int32_t n_seg_o
     } else {
         blocks = rows * stats_blocks(row_size);
     }
-    return blocks * 32;
+    // one segment: room for the one-launch form (barrier words + partials)
+    const bool one_seg = n_seg_offsets == 2 || (n_seg_offsets == 0 && rows == 1);
+    return one_seg && blocks * 32 < kFuseBytes ? kFuseBytes : blocks * 32;
 }
 
 // builtin: the statistics go to the library's per-device scratch instead of
@@ -821,6 +823,15 @@ static int32_t euler_step(const void* x_t, const void* v_pos, const void* v_neg,
         a.nblocks = blocks;
         a.nstats = stats;
         a.vec = al && bounds_al ? 1 : 0;
+        // one segment on whole vectors with room for the barrier: the
+        // launcher may take the one-launch form
+        const bool one_seg = n_seg_offsets > 0 ? a.nseg == 1 : rows == 1;
+        if (one_seg && a.vec && workspace_bytes >= kFuseBytes) {
+            a.fuse = 1;
+            a.fuse_lo = n_seg_offsets > 0 ? a.bounds[0] : 0;
+            a.fuse_hi = n_seg_offsets > 0 ? a.bounds[1] : n;
+            a.fuse_ws = workspace;
+        }
     } else {
         a.nblocks = (n + kEulerChunk - 1) / kEulerChunk;
         a.vec = al && n % ve == 0 ? 1 : 0;

@@ -171,6 +171,16 @@ constexpr int kEulerScratchPartials = kEulerMaxSeg * kStatsMaxPerSeg;
 static_assert(kEulerChunk % (kEulerBlock * 8) == 0, "T2H_EULER_CHUNK: a multiple of 8 * kEulerBlock");
 static_assert(kStatsPer % 8 == 0, "T2H_STATS_PER: whole 16-byte vectors of every storage type");
 static_assert(kStatsBlock % 64 == 0 && kStatsBlock <= 1024, "T2H_STATS_BLOCK: whole waves, one block");
+// One-launch rescale (a single segment whose three tensors fit in the
+// registers of one resident grid): the workspace starts with the grid
+// barrier's words (kEulerBarBytes: an error word, 8 release slots of 128
+// bytes, one 64-bit arrival flag per block), then one f64 partial quad per
+// block.
+constexpr int kFuseBlock = 256;           // threads per block
+constexpr int kFuseMaxBlocks = 4096;      // blocks (partials) the workspace is sized for
+constexpr int kEulerBarBytes = 64 + 8 * 128 + kFuseMaxBlocks * 8;
+constexpr int64_t kFuseBytes = kEulerBarBytes + (int64_t)kFuseMaxBlocks * 32;
+static_assert(kFuseBytes <= (int64_t)kEulerScratchPartials * 32, "the built-in scratch holds the one-launch form");
 struct EulerArgs {
     const void* x;
     const void* v_pos;
@@ -195,6 +205,12 @@ struct EulerArgs {
     int64_t nblocks;         // blocks of the elementwise pass
     int64_t nstats;          // blocks of the statistics pass (= f64 partials)
     double* partial;         // [nstats][4] workspace: sum x0_pos, sum x0_pos^2, sum x0_cfg, sum x0_cfg^2
+    // one-launch rescale: set by the host when the call may take it (one
+    // segment [fuse_lo, fuse_hi) on whole vectors, a workspace of kFuseBytes);
+    // the launcher takes it when the segment fits the resident grid
+    int32_t fuse;
+    int64_t fuse_lo, fuse_hi;
+    void* fuse_ws;           // the workspace: barrier words, then the partial quads
 };
 
 struct PhaseArgs {

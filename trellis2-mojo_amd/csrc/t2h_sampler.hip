@@ -14,7 +14,13 @@
 // Segments are rows of row_size elements (dense state, unbiased std) or the
 // caller's token segments (varlen state, biased std).
 //
-// The rescale takes two launches:
+// The rescale of a single segment on whole 16-byte vectors whose three
+// tensors fit in the registers of the resident grid (the config-5 latent:
+// 6.4M f32 elements, 4 vectors of each tensor per thread) takes one launch,
+// euler_fused_kernel: it loads the three inputs once, publishes per-block
+// sums, meets the other blocks at a grid barrier and stores (see there).
+// Otherwise (several segments, larger states, a workspace without room for
+// the barrier) the rescale takes two launches:
 // - euler_stats_kernel: one block of 1024 threads per 16,384 elements of a
 //   segment, at most kStatsMaxPerSeg, take equal shares of it, load them with
 //   16-byte loads (16 elements of each tensor per thread per load group), sum
@@ -178,6 +184,23 @@ __global__ __launch_bounds__(kStatsBlock) void euler_stats_kernel(EulerArgs a) {
     }
 }
 
+// std(x0_pos) / std(x0_cfg) of a segment of m elements from its four sums:
+// unbiased for a dense row, biased (mean(x^2) - mean(x)^2) for a varlen
+// segment.
+__device__ __forceinline__ float ratio_of_sums(const double (&acc)[4], int64_t m, bool unbiased) {
+    const double md = (double)m;
+    double vp, vc;
+    if (unbiased) {
+        vp = (acc[1] - acc[0] * (acc[0] / md)) / (md - 1.0);
+        vc = (acc[3] - acc[2] * (acc[2] / md)) / (md - 1.0);
+    } else {
+        vp = acc[1] / md - (acc[0] / md) * (acc[0] / md);
+        vc = acc[3] / md - (acc[2] / md) * (acc[2] / md);
+    }
+    if (unbiased && m == 1) return __builtin_nanf("");   // 0/0 as the reference's m - 1 = 0
+    return (float)(sqrt(vp > 0.0 ? vp : 0.0) / sqrt(vc > 0.0 ? vc : 0.0));
+}
+
 // The rescale ratio of segment s from its partials (called by every thread
 // of a kEulerBlock-thread block; the same bits in every block).
 __device__ __forceinline__ float segment_ratio(const EulerArgs& a, int s, double (*sh)[4]) {
@@ -198,17 +221,7 @@ __device__ __forceinline__ float segment_ratio(const EulerArgs& a, int s, double
         acc[0] += u.x; acc[1] += u.y; acc[2] += w.x; acc[3] += w.y;
     }
     block_sum4<kEulerBlock / 64>(acc, sh);
-    const double md = (double)m;
-    double vp, vc;
-    if (a.uniform) {   // unbiased, one segment per row
-        vp = (acc[1] - acc[0] * (acc[0] / md)) / (md - 1.0);
-        vc = (acc[3] - acc[2] * (acc[2] / md)) / (md - 1.0);
-    } else {           // biased: mean(x^2) - mean(x)^2
-        vp = acc[1] / md - (acc[0] / md) * (acc[0] / md);
-        vc = acc[3] / md - (acc[2] / md) * (acc[2] / md);
-    }
-    if (a.uniform && m == 1) return __builtin_nanf("");   // 0/0 as the reference's m - 1 = 0
-    return (float)(sqrt(vp > 0.0 ? vp : 0.0) / sqrt(vc > 0.0 ? vc : 0.0));
+    return ratio_of_sums(acc, m, a.uniform != 0);
 }
 
 template <int MODE>
@@ -293,6 +306,259 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
     }
 }
 
+// The one-launch rescale over a single segment [fuse_lo, fuse_hi) of whole
+// 16-byte vectors. Each data block holds KV vectors of each tensor per
+// thread, in registers, from the first load to the last store:
+// 1. load x, v_pos, v_neg; sum the block's four x0 sums (f64, fixed order),
+//    publish them as the block's partial quad and raise the block's flag;
+// 2. one extra block, which holds no vectors, waits for every flag, sums
+//    the quads in a fixed order into the ratio (the same bits on every
+//    call) and publishes it in 8 release slots, 128 bytes apart, which the
+//    data blocks poll in turn (block b polls slot b % 8);
+// 3. every data block applies the step to the vectors it holds and stores.
+// No two blocks update one word (same-address atomics from ~1,600 blocks
+// serialize). Each slot carries a 64-bit epoch: a launch reads it (e), its
+// blocks raise their flags to e + 1 and the reducing block sets the slot
+// to e + 1. Flags left by earlier launches hold at most e, so the
+// workspace needs no clearing and a graph replay reads the epoch the last
+// launch left; a first use on uninitialised memory is safe unless a flag
+// happens to hold e + 1 (64-bit values: chance 2^-64 per flag).
+// The launcher sizes the grid to be resident at once (occupancy x CUs), so
+// every block arrives; a block that still waits after 2^20 polls (each a
+// device-coherent load and a short sleep: about a second) stops waiting,
+// sets `err` and goes on (the output is then wrong, but the grid drains).
+struct EulerSlot {
+    uint64_t epoch;   // e at the launch; e + 1 once `ratio` is out
+    float ratio;
+    unsigned pad[29];
+};
+struct EulerBar {
+    uint64_t err;     // set to e + 1 of slot 0 by a block that stopped waiting
+    uint64_t pad[7];
+    EulerSlot slot[8];
+    uint64_t flag[kFuseMaxBlocks];   // e + 1 of the block's slot once its quad is out
+};
+static_assert(sizeof(EulerSlot) == 128, "one slot per 128 bytes");
+static_assert(sizeof(EulerBar) == kEulerBarBytes, "barrier words");
+
+__device__ __forceinline__ uint64_t shared_load(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void shared_store(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack16(const u32x4& w, float* f) {
+    constexpr int WN = Word<T>::N;
+    Word<T>::unpack(w.x, f);
+    Word<T>::unpack(w.y, f + WN);
+    Word<T>::unpack(w.z, f + 2 * WN);
+    Word<T>::unpack(w.w, f + 3 * WN);
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack16(const float* f) {
+    constexpr int WN = Word<T>::N;
+    u32x4 w;
+    w.x = Word<T>::pack(f);
+    w.y = Word<T>::pack(f + WN);
+    w.z = Word<T>::pack(f + 2 * WN);
+    w.w = Word<T>::pack(f + 3 * WN);
+    return w;
+}
+
+constexpr int kFusePolls = 1 << 20;
+
+
+// Every word the blocks of euler_fused_kernel share (partial quads, flags,
+// release slots) is written and read as a device-scope relaxed atomic: a
+// device-coherent access that no XCD's L2 holds stale. The wave's own stores
+// are ordered by waiting for them before the store that publishes them (no
+// agent-scope fence: its L2 write-back and invalidate would run on every
+// block's L2 and cost more than the step). The readers issue their loads
+// after the load that saw the flag.
+__device__ __forceinline__ double shared_load(const double* p) {
+    return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_after_stores() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // no compiler reordering across it
+    __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0): the wave's stores are done
+}
+
+template <typename T, int KV>
+__global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
+    constexpr int V = kPack<T>;
+    constexpr int NW = kFuseBlock / 64;
+    __shared__ double sh[NW][4];
+    __shared__ float ratio_s;
+    EulerBar* bar = static_cast<EulerBar*>(a.fuse_ws);
+    double* partial = reinterpret_cast<double*>(static_cast<char*>(a.fuse_ws) + kEulerBarBytes);
+    const unsigned nblk = gridDim.x - 1;   // data blocks; the last block reduces
+    if (blockIdx.x == nblk) {
+        // wait for every data block's flag, sum their quads in a fixed order
+        // (the same bits on every call), publish the ratio. The flags this
+        // thread reads (i = threadIdx.x + j * kFuseBlock) all belong to slot
+        // threadIdx.x % 8.
+        const uint64_t want = shared_load(&bar->slot[threadIdx.x % 8].epoch) + 1;
+        double t[4] = {0.0, 0.0, 0.0, 0.0};
+        bool all = false;
+        for (int it = 0; it < kFusePolls && !all; ++it) {
+            int mine = 1;
+#pragma unroll
+            for (int j = 0; j < kFuseMaxBlocks / kFuseBlock; ++j) {
+                // every flag load in flight at once: unconditional, indices
+                // past the last data block read its flag again and ignore it
+                // (its slot, and so its epoch, can differ from this thread's)
+                const unsigned i = threadIdx.x + j * kFuseBlock;
+                const uint64_t f = shared_load(&bar->flag[i < nblk ? i : nblk - 1]);
+                mine &= (i >= nblk) | (f == want);
+            }
+            all = __syncthreads_and(mine) != 0;
+            if (!all) __builtin_amdgcn_s_sleep(1);
+        }
+        if (!all && threadIdx.x == 0) shared_store(&bar->err, want);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        for (unsigned i0 = threadIdx.x; i0 < nblk; i0 += 4 * kFuseBlock) {
+            // quads i0, i0 + kFuseBlock, ... in that (fixed) order, four loads
+            // in flight at once
+            double q[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const unsigned i = i0 + u * kFuseBlock;
+                const double* p = partial + (int64_t)(i < nblk ? i : nblk - 1) * 4;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) q[u][c] = shared_load(p + c);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (i0 + u * kFuseBlock < nblk) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) t[c] += q[u][c];
+                }
+            }
+        }
+        block_sum4<NW>(t, sh);
+        if (threadIdx.x < 8) {
+            const float r = ratio_of_sums(t, a.fuse_hi - a.fuse_lo, a.uniform != 0);
+            __hip_atomic_store(&bar->slot[threadIdx.x].ratio, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            publish_after_stores();
+            shared_store(&bar->slot[threadIdx.x].epoch, want);
+        }
+        return;
+    }
+    const int64_t nv = (a.fuse_hi - a.fuse_lo) / V;
+    // buffer descriptors over the segment: a 32-bit byte offset per vector
+    // serves the three tensors and the two outputs, and the descriptor's
+    // range check (on the offset register) makes loads past the segment read
+    // 0 and drops stores past it
+    const int bytes = (int)(nv * 16);
+    auto rsrc = [&](const void* p) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(static_cast<const T*>(p) + a.fuse_lo), 0, bytes,
+                                                 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x), rp = rsrc(a.v_pos), rn = rsrc(a.v_neg);
+    const int blk0 = (int)blockIdx.x * kFuseBlock * KV;   // first vector of the block
+    auto voff = [&](int k) { return (blk0 + k * kFuseBlock + (int)threadIdx.x) * 16; };
+    EulerSlot* sl = &bar->slot[blockIdx.x % 8];
+    uint64_t e0 = 0;   // the slot's epoch at the launch
+    if (threadIdx.x == 0) e0 = shared_load(&sl->epoch);
+    u32x4 xw[KV], pw[KV], nw[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        // non-temporal (aux 2): each vector is read once (26.2 against 27.7 us
+        // with the default policy, config-5 latent)
+        xw[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, voff(k), 0, 2);
+        pw[k] = __builtin_amdgcn_raw_buffer_load_b128(rp, voff(k), 0, 2);
+        nw[k] = __builtin_amdgcn_raw_buffer_load_b128(rn, voff(k), 0, 2);
+    }
+    const int64_t my0 = blk0 + (int64_t)threadIdx.x;   // this thread's first vector
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        if (my0 + (int64_t)k * kFuseBlock < nv) {
+            float xf[V], pf[V], nf[V];
+            unpack16<T>(xw[k], xf);
+            unpack16<T>(pw[k], pf);
+            unpack16<T>(nw[k], nf);
+#pragma unroll
+            for (int i = 0; i < V; ++i) stats_add(a, xf[i], pf[i], nf[i], acc);
+        }
+    }
+    // the block's quad: wave sums, then lanes 0-3 of wave 0 add the waves'
+    // values in wave order (few registers beside the held vectors)
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const double t = wave_sum_d(acc[c]);
+        if ((threadIdx.x & 63) == 0) sh[w][c] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        double q = sh[0][threadIdx.x];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) q += sh[i][threadIdx.x];
+        __hip_atomic_store(partial + (int64_t)blockIdx.x * 4 + threadIdx.x, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        publish_after_stores();   // the quad is out before the flag
+        if (threadIdx.x == 0) shared_store(&bar->flag[blockIdx.x], e0 + 1);
+    }
+    if (threadIdx.x == 0) {
+        bool done = false;
+        for (int it = 0; it < kFusePolls && !done; ++it) {
+            done = shared_load(&sl->epoch) != e0;
+            if (!done) __builtin_amdgcn_s_sleep(2);
+        }
+        if (!done) shared_store(&bar->err, e0 + 1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        ratio_s = __hip_atomic_load(&sl->ratio, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const float ratio = ratio_s;
+    // only the loaded words stay live across the barrier: the products the
+    // statistics formed are formed again (kept, they would double the
+    // registers a thread holds and halve the resident grid)
+#pragma unroll
+    for (int k = 0; k < KV; ++k) asm volatile("" : "+v"(xw[k]), "+v"(pw[k]), "+v"(nw[k]));
+    const __amdgpu_buffer_rsrc_t ro = rsrc(a.x_prev);
+    const __amdgpu_buffer_rsrc_t rz = rsrc(a.pred_x0 != nullptr ? a.pred_x0 : a.x_prev);
+    constexpr int kStoreAux = T2H_EULER_NTS ? 2 : 0;   // 2: the non-temporal bit
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        if (my0 + (int64_t)k * kFuseBlock < nv) {
+            float xf[V], pf[V], nf[V], o[V], z[V];
+            unpack16<T>(xw[k], xf);
+            unpack16<T>(pw[k], pf);
+            unpack16<T>(nw[k], nf);
+#pragma unroll
+            for (int i = 0; i < V; ++i) apply_elem<2>(a, ratio, xf[i], pf[i], nf[i], o[i], z[i]);
+            __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(o), ro, voff(k), 0, kStoreAux);
+            if (a.pred_x0 != nullptr) __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(z), rz, voff(k), 0, kStoreAux);
+        }
+    }
+}
+
+// Blocks of euler_fused_kernel<T, KV> resident at once on this device.
+template <typename T, int KV>
+int64_t fused_capacity() {
+    static const int64_t cap = [] {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, euler_fused_kernel<T, KV>, kFuseBlock, 0) !=
+                hipSuccess || nb <= 0)
+            return (int64_t)0;
+        return (int64_t)nb * device_cu_count();
+    }();
+    return cap;
+}
+
+template <typename T, int KV>
+bool try_fused(const EulerArgs& a, hipStream_t st) {
+    const int64_t nv = (a.fuse_hi - a.fuse_lo) / kPack<T>;
+    const int64_t g = (nv + (int64_t)kFuseBlock * KV - 1) / ((int64_t)kFuseBlock * KV);
+    if (g > kFuseMaxBlocks || g + 1 > fused_capacity<T, KV>()) return false;
+    hipLaunchKernelGGL((euler_fused_kernel<T, KV>), dim3((unsigned)(g + 1)), dim3(kFuseBlock), 0, st, a);
+    return true;
+}
+
 // Rows outside every varlen segment: the reference's rescale leaves their
 // prediction at zero, so x_prev = x and pred_x0 = fl(x * a).
 template <typename T>
@@ -311,7 +577,13 @@ __global__ __launch_bounds__(kEulerBlock) void euler_uncovered_kernel(EulerArgs 
 template <typename T>
 hipError_t launch_typed(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, hipStream_t st) {
     if (a.mode == 2) {
-        if (a.nblocks > 0) {
+        // one launch when the segment fits the resident grid with 1, 2, 4 or
+        // 8 vectors of each tensor per thread; else the statistics pass and
+        // the elementwise pass
+        const bool fused = a.fuse && a.fuse_hi > a.fuse_lo &&
+                           (try_fused<T, 1>(a, st) || try_fused<T, 2>(a, st) || try_fused<T, 4>(a, st) ||
+                            try_fused<T, 8>(a, st));
+        if (!fused && a.nblocks > 0) {
             hipLaunchKernelGGL(euler_stats_kernel<T>, grid_1d(a.nstats), dim3(kStatsBlock), 0, st, a);
             hipLaunchKernelGGL((euler_apply_kernel<T, 2>), grid_1d(a.nblocks), dim3(kEulerBlock), 0, st, a);
         }
@@ -340,8 +612,9 @@ hipError_t launch_typed(const EulerArgs& a, int64_t cover_lo, int64_t cover_hi, 
 // stand-in, not a device address): euler_scratch() looks the device address
 // up with hipGetSymbolAddress once per device and every launch takes that.
 // Every statistics block writes its quad before the elementwise pass reads
-// it, so nothing has to start at zero; calls that overlap on one GPU share
-// the array and race.
+// it, and the one-launch form's barrier words work from any contents, so
+// nothing has to start at zero; calls that overlap on one GPU share the
+// array and race.
 __device__ __align__(256) double scratch[kEulerScratchPartials * 4];
 
 }  // namespace
