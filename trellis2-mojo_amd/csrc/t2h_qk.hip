@@ -41,7 +41,7 @@ constexpr int kWaves = kBlock / 64;
 constexpr int kTileWaves = T2H_QK_WAVES;   // token rows (one per wave) per tile block
 constexpr int kSmallTileWaves = 4;         // ... when the launch is short of rows (launch_fast)
 
-template <typename T, int D, int NG, int W>
+template <typename T, int D, int NG, int W, bool EARLY>
 __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab) {
     using L = HeadLanes<T, D>;
     constexpr int E = L::E;
@@ -105,13 +105,15 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     const float* __restrict__ bias = which == 0 ? a.bias_q : a.bias_k;
     const PosSource src{a.coords, a.coord_cols, a.grid_res, a.pos_dim};
 
-    // 16-bit rows: the slot's frequency and the block's gamma / bias values
-    // are loaded before the row loads, so the phase and the LDS staging wait
-    // for them alone and run while the rows are in flight (MI355X, config 5:
-    // 414 -> 401 us). f32 keeps its parameter loads after the row loads:
-    // there the early order left the row loads behind an extra wait (config
-    // 2: 17.7 -> 31.9 us).
-    constexpr bool kEarly = sizeof(T) == 2;
+    // EARLY (16-bit rows; f32 rows with a bias or in 8-row tiles): the slot's
+    // frequency and the block's gamma / bias values are loaded before the
+    // row loads, so the phase and the LDS staging wait for them alone and run
+    // while the rows are in flight (MI355X, config 5: 414 -> 401 us; the
+    // small-T block's packed f32 qkv 116.1 -> 114.4 us per block; config 4's
+    // f32 QK 163.8 -> 160.6 us). f32 4-row tiles without a bias keep their
+    // parameter loads after the row loads (config 2: 17.7 against 20.8 us
+    // early).
+    constexpr bool kEarly = EARLY;
     const int my_slot = lane % HALF;
     // 16-bit rows: the slot's axis from its index, so the coordinate load goes
     // out without waiting for a table load (config 5: 402 -> 398 us)
@@ -330,8 +332,16 @@ hipError_t launch_fast(QkArgs a, const RopeSlots& tab, hipStream_t s) {
     const int64_t tiles = (a.rows + w - 1) / w;
     a.fper = front_per(tiles);
     const dim3 grid = grid_1d(front_grid(tiles) * upr);
-    if (small) hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kSmallTileWaves>), grid, dim3(kSmallTileWaves * 64), 0, s, a, tab);
-    else hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kTileWaves>), grid, dim3(kTileWaves * 64), 0, s, a, tab);
+    if constexpr (sizeof(T) == 2) {
+        if (small) hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kSmallTileWaves, true>), grid, dim3(kSmallTileWaves * 64), 0, s, a, tab);
+        else hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kTileWaves, true>), grid, dim3(kTileWaves * 64), 0, s, a, tab);
+    } else if (a.bias_q != nullptr || a.bias_k != nullptr || !small) {
+        if (small) hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kSmallTileWaves, true>), grid, dim3(kSmallTileWaves * 64), 0, s, a, tab);
+        else hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kTileWaves, true>), grid, dim3(kTileWaves * 64), 0, s, a, tab);
+    } else {
+        if (small) hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kSmallTileWaves, false>), grid, dim3(kSmallTileWaves * 64), 0, s, a, tab);
+        else hipLaunchKernelGGL((qk_tile_kernel<T, D, NG, kTileWaves, false>), grid, dim3(kTileWaves * 64), 0, s, a, tab);
+    }
     return hipGetLastError();
 }
 
