@@ -77,15 +77,22 @@ def test_noalloc_rejects_states_beyond_its_scratch(dev):
     assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
 
 
-def test_noalloc_step_in_a_hip_graph(dev):
+@pytest.mark.parametrize("which", ["config4_two_segments", "config5_one_segment"])
+def test_noalloc_step_in_a_hip_graph(dev, which):
     """The entry point's purpose: a sampler step recorded into a HIP graph.
     t2h_device_init did the scratch lookup, so the call only enqueues its
     kernels. Three replays with fresh inputs, eager no-allocation calls in
     between (which reuse the same scratch), each equal to the workspace entry
-    point's result bit for bit."""
-    _, off4 = workloads.config4()
-    segs = off4.tolist()
-    x, vp, vn = _state(4040, (int(off4[-1]), 32), dev)
+    point's result bit for bit. Two segments take the statistics pass and
+    the elementwise pass; the config-5 latent as one segment takes the
+    one-launch form, whose grid barrier lives in the same scratch."""
+    if which == "config4_two_segments":
+        _, off = workloads.config4()
+        segs = off.tolist()
+    else:
+        _, off = workloads.config5()
+        segs = [0, int(off[-1])]
+    x, vp, vn = _state(4040, (int(off[-1]), 32), dev)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
