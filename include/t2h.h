@@ -349,9 +349,11 @@ int32_t t2h_gate_residual_ln_modulate(
  * segment (rows == 1 dense, or two seg offsets) on whole 16-byte vectors
  * and a workspace of that size, a state that fits the registers of the
  * resident grid (up to ~7M f32 elements on MI355X) is rescaled in one
- * launch whose blocks meet at a grid barrier in the workspace; a smaller
- * workspace (at least the statistics partials', as the error names) gives
- * the two-launch form. */
+ * launch whose blocks meet at a grid barrier in the workspace; its result
+ * does not depend on other streams' work (a block that cannot be resident
+ * in time leaves its share to the grid's reducing block, which only costs
+ * time). A smaller workspace (at least the statistics partials', as the
+ * error names) gives the two-launch form. */
 int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size,
                                  int32_t n_seg_offsets);
 int32_t t2h_flow_euler_step(const void* x_t, const void* v_pos,

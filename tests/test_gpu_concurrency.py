@@ -78,3 +78,48 @@ def test_two_threads_two_streams_bit_exact(dev):
         assert len(got[j]) == len(want[j])
         for a, b in zip(got[j], want[j]):
             assert torch.equal(a, b), f"thread {j}: an op differs from the single-stream result"
+
+
+def test_one_launch_rescale_on_two_streams(dev):
+    """The one-launch rescale sizes its grid to fill the GPU and meets at a
+    grid barrier. Two host threads each enqueue it on a stream of their own
+    (config-5-sized latents, one segment each), interleaved, so the two grids
+    compete for the CUs; blocks that are not resident in time leave their
+    vectors to their grid's reducing block. Bit for bit the results of the
+    same steps one at a time on the default stream."""
+    T = 201436
+    g = torch.Generator(device=dev).manual_seed(103)
+    states = [[torch.randn((T, 32), generator=g, device=dev) for _ in range(3)] for _ in range(2)]
+    wss = [torch.empty(ops.flow_euler_workspace(T, 32, 2), dtype=torch.uint8, device=dev) for _ in range(2)]
+
+    def step(j):
+        x, vp, vn = states[j]
+        return ops.flow_euler_step(x, vp, 0.7, 0.6, 1e-5, v_neg=vn, guidance_strength=3.0, guidance_rescale=0.5,
+                                   seg_offsets=[0, T], workspace=wss[j])
+
+    want = [step(j) for j in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev) for _ in range(2)]   # default priority
+    got, errors = [None, None], []
+    start = threading.Barrier(2)
+
+    def worker(j):
+        try:
+            start.wait()
+            with torch.cuda.stream(streams[j]):
+                res = None
+                for _ in range(16):
+                    res = step(j)
+                streams[j].synchronize()
+                got[j] = res
+        except Exception as e:   # noqa: BLE001 - reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for j in range(2):
+        assert torch.equal(got[j][0], want[j][0]) and torch.equal(got[j][1], want[j][1]), f"thread {j}"

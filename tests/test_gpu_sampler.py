@@ -166,9 +166,9 @@ def test_step_rescale_config5_latent(dev, dtype):
 
 # the workspace of the one-launch rescale: the barrier words (a 64-bit error
 # word in the first 64 bytes, 8 release slots of 128 bytes each starting with
-# a 64-bit epoch, one 64-bit arrival flag per block for up to 4096 blocks),
-# then one f64 quad per block
-FUSE_BYTES = 64 + 8 * 128 + 4096 * 8 + 4096 * 32
+# a 64-bit epoch, then per block, for up to 2048 blocks, a 64-bit arrival
+# flag, leave mark and claim word), then one f64 quad per block
+FUSE_BYTES = 64 + 8 * 128 + 3 * 2048 * 8 + 2048 * 32
 
 
 def _step(x, p, n, t, tp, g, gr, segs, ws):
@@ -228,6 +228,30 @@ def test_step_rescale_one_launch_repeats_on_a_dirty_workspace(dev):
         assert int(words[0]) != epochs[0], "error word"
     for o in outs[1:]:
         assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1])
+
+
+@pytest.mark.parametrize("polls", ["0", "1"])
+def test_step_rescale_one_launch_blocks_that_leave(dev, polls, monkeypatch):
+    """A data block that waits too long for the ratio (its grid not resident
+    at once) leaves its vectors to the reducing block. Forced from the host
+    with T2H_FUSE_WAIT_POLLS = 0 or 1 (every block, or nearly every, leaves):
+    the same bits as the normal launch, also with x_prev aliasing x_t (a
+    left vector is stored once, by one of the two), and the error word
+    stays unequal to the new epoch."""
+    T = 201436
+    x, pos, neg = (to_dev(a, dev) for a in _case(4300, (T, 32)))
+    ws = torch.empty(FUSE_BYTES, dtype=torch.uint8, device=dev)
+    want = _step(x, pos, neg, 0.8, 0.72, 3.0, 0.6, [0, T], ws)
+    monkeypatch.setenv("T2H_FUSE_WAIT_POLLS", polls)
+    for _ in range(2):
+        got = _step(x, pos, neg, 0.8, 0.72, 3.0, 0.6, [0, T], ws)
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+        words = ws[:64 + 8 * 128].view(torch.int64).cpu()
+        assert int(words[0]) != int(words[8]), "error word"
+    xi = x.clone()
+    _, x0 = ops.flow_euler_step(xi, pos, 0.8, 0.72, SM, v_neg=neg, guidance_strength=3.0, guidance_rescale=0.6,
+                                seg_offsets=[0, T], workspace=ws, x_prev=xi)
+    assert torch.equal(xi, want[0]) and torch.equal(x0, want[1])
 
 
 def test_step_rescale_one_launch_in_a_hip_graph(dev):

@@ -15,6 +15,8 @@
 #include <vector>
 
 #include "t2h.h"
+#include <cstdlib>
+
 #include "t2h_internal.h"
 
 namespace t2h {
@@ -728,6 +730,17 @@ int64_t t2h_flow_euler_workspace(int64_t rows, int64_t row_size, int32_t n_seg_o
     return one_seg && blocks * 32 < kFuseBytes ? kFuseBytes : blocks * 32;
 }
 
+// Polls a data block of the one-launch rescale waits for the ratio before it
+// leaves its vectors to the reducing block (a normal wait takes tens). The
+// environment's T2H_FUSE_WAIT_POLLS overrides it, read on every call: 0
+// makes every block leave, which the tests use to run that path.
+static int32_t fuse_wait_polls() {
+    const char* e = std::getenv("T2H_FUSE_WAIT_POLLS");
+    if (e == nullptr || *e == '\0') return 1 << 12;
+    const long v = std::strtol(e, nullptr, 10);
+    return v < 0 ? 0 : (v > (1 << 20) ? (1 << 20) : (int32_t)v);
+}
+
 // builtin: the statistics go to the library's per-device scratch instead of
 // the caller's workspace (t2h_flow_euler_step_noalloc).
 static int32_t euler_step(const void* x_t, const void* v_pos, const void* v_neg, void* x_prev, void* pred_x0,
@@ -831,6 +844,7 @@ static int32_t euler_step(const void* x_t, const void* v_pos, const void* v_neg,
             a.fuse_lo = n_seg_offsets > 0 ? a.bounds[0] : 0;
             a.fuse_hi = n_seg_offsets > 0 ? a.bounds[1] : n;
             a.fuse_ws = workspace;
+            a.fuse_polls = fuse_wait_polls();
         }
     } else {
         a.nblocks = (n + kEulerChunk - 1) / kEulerChunk;

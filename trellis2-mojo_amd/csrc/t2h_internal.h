@@ -174,11 +174,12 @@ static_assert(kStatsBlock % 64 == 0 && kStatsBlock <= 1024, "T2H_STATS_BLOCK: wh
 // One-launch rescale (a single segment whose three tensors fit in the
 // registers of one resident grid): the workspace starts with the grid
 // barrier's words (kEulerBarBytes: an error word, 8 release slots of 128
-// bytes, one 64-bit arrival flag per block), then one f64 partial quad per
-// block.
+// bytes, and per block a 64-bit arrival flag, a leave mark and a claim
+// word), then one f64 partial quad per block.
 constexpr int kFuseBlock = 256;           // threads per block
-constexpr int kFuseMaxBlocks = 4096;      // blocks (partials) the workspace is sized for
-constexpr int kEulerBarBytes = 64 + 8 * 128 + kFuseMaxBlocks * 8;
+constexpr int kFuseMaxBlocks = 2048;      // blocks (partials) the workspace is sized for: the most
+                                          // 256-thread blocks 256 CUs hold at once (8 per CU)
+constexpr int kEulerBarBytes = 64 + 8 * 128 + 3 * kFuseMaxBlocks * 8;
 constexpr int64_t kFuseBytes = kEulerBarBytes + (int64_t)kFuseMaxBlocks * 32;
 static_assert(kFuseBytes <= (int64_t)kEulerScratchPartials * 32, "the built-in scratch holds the one-launch form");
 struct EulerArgs {
@@ -209,6 +210,7 @@ struct EulerArgs {
     // segment [fuse_lo, fuse_hi) on whole vectors, a workspace of kFuseBytes);
     // the launcher takes it when the segment fits the resident grid
     int32_t fuse;
+    int32_t fuse_polls;      // polls a data block waits for the ratio before it leaves its vectors
     int64_t fuse_lo, fuse_hi;
     void* fuse_ws;           // the workspace: barrier words, then the partial quads
 };

@@ -321,22 +321,31 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
 // blocks raise their flags to e + 1 and the reducing block sets the slot
 // to e + 1. Flags left by earlier launches hold at most e, so the
 // workspace needs no clearing and a graph replay reads the epoch the last
-// launch left; a first use on uninitialised memory is safe unless a flag
-// happens to hold e + 1 (64-bit values: chance 2^-64 per flag).
-// The launcher sizes the grid to be resident at once (occupancy x CUs), so
-// every block arrives; a block that still waits after 2^20 polls (each a
-// device-coherent load and a short sleep: about a second) stops waiting,
-// sets `err` and goes on (the output is then wrong, but the grid drains).
+// launch left; a first use on uninitialised memory is safe unless a word
+// happens to hold e + 1 (64-bit values: chance 2^-64 per word).
+// The launcher sizes the grid to be resident at once (occupancy x CUs). A
+// grid that is not (other streams' kernels hold part of the GPU) still
+// finishes with the same result: a data block that has waited fuse_polls
+// polls for the ratio marks its vectors left and exits, which frees its
+// slot for the blocks not yet running; the reducing block then loads the
+// left vectors from memory and stores them. A block that sees the ratio
+// right after marking takes its vectors back; one exchange on the block's
+// claim word decides which of the two stores them, so no vector is
+// computed twice (x_prev may alias x_t). The reducing block's own wait is
+// bounded too (2^20 polls, about a second): past it, it sets `err` and goes
+// on, so the grid always drains.
 struct EulerSlot {
     uint64_t epoch;   // e at the launch; e + 1 once `ratio` is out
     float ratio;
     unsigned pad[29];
 };
 struct EulerBar {
-    uint64_t err;     // set to e + 1 of slot 0 by a block that stopped waiting
+    uint64_t err;     // set to e + 1 by the reducing block if it stopped waiting
     uint64_t pad[7];
     EulerSlot slot[8];
-    uint64_t flag[kFuseMaxBlocks];   // e + 1 of the block's slot once its quad is out
+    uint64_t flag[kFuseMaxBlocks];    // e + 1 of the block's slot once its quad is out
+    uint64_t leave[kFuseMaxBlocks];   // e + 1 once the block has stopped waiting for the ratio
+    uint64_t claim[kFuseMaxBlocks];   // exchanged to e + 1 by whoever stores a left block's vectors
 };
 static_assert(sizeof(EulerSlot) == 128, "one slot per 128 bytes");
 static_assert(sizeof(EulerBar) == kEulerBarBytes, "barrier words");
@@ -346,6 +355,10 @@ __device__ __forceinline__ uint64_t shared_load(const uint64_t* p) {
 }
 __device__ __forceinline__ void shared_store(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// true for the first caller of a launch (the word held anything but v)
+__device__ __forceinline__ bool claim_first(uint64_t* p, uint64_t v) {
+    return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != v;
 }
 
 template <typename T>
@@ -390,31 +403,84 @@ template <typename T, int KV>
 __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
     constexpr int V = kPack<T>;
     constexpr int NW = kFuseBlock / 64;
+    constexpr int NJ = kFuseMaxBlocks / kFuseBlock;   // block-index groups a reducing thread covers
     __shared__ double sh[NW][4];
     __shared__ float ratio_s;
+    __shared__ unsigned own_s;                        // data block: 1 = store the held vectors
+    __shared__ unsigned long long left_s[NJ][NW];    // reducing block: ballots of the left blocks
+    __shared__ uint64_t want_s[8];                   // reducing block: each slot's new epoch
     EulerBar* bar = static_cast<EulerBar*>(a.fuse_ws);
     double* partial = reinterpret_cast<double*>(static_cast<char*>(a.fuse_ws) + kEulerBarBytes);
     const unsigned nblk = gridDim.x - 1;   // data blocks; the last block reduces
+    const int64_t nv = (a.fuse_hi - a.fuse_lo) / V;
+    // buffer descriptors over the segment: a 32-bit byte offset per vector
+    // serves the three tensors and the two outputs, and the descriptor's
+    // range check (on the offset register) makes loads past the segment read
+    // 0 and drops stores past it
+    const int bytes = (int)(nv * 16);
+    auto rsrc = [&](const void* p) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(static_cast<const T*>(p) + a.fuse_lo), 0, bytes,
+                                                 0x00020000);
+    };
+    // vector k of this thread in data block blk
+    auto vec = [&](unsigned blk, int k) { return (int64_t)blk * kFuseBlock * KV + k * kFuseBlock + threadIdx.x; };
+    auto load_block = [&](unsigned blk, u32x4 (&xw)[KV], u32x4 (&pw)[KV], u32x4 (&nw)[KV]) {
+        const __amdgpu_buffer_rsrc_t rx = rsrc(a.x), rp = rsrc(a.v_pos), rn = rsrc(a.v_neg);
+#pragma unroll
+        for (int k = 0; k < KV; ++k) {
+            // non-temporal (aux 2): each vector is read once (26.2 against
+            // 27.7 us with the default policy, config-5 latent)
+            const int off = (int)(vec(blk, k) * 16);
+            xw[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 2);
+            pw[k] = __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 2);
+            nw[k] = __builtin_amdgcn_raw_buffer_load_b128(rn, off, 0, 2);
+        }
+    };
+    auto store_block = [&](unsigned blk, float ratio, const u32x4 (&xw)[KV], const u32x4 (&pw)[KV],
+                           const u32x4 (&nw)[KV]) {
+        const __amdgpu_buffer_rsrc_t ro = rsrc(a.x_prev);
+        const __amdgpu_buffer_rsrc_t rz = rsrc(a.pred_x0 != nullptr ? a.pred_x0 : a.x_prev);
+        constexpr int kStoreAux = T2H_EULER_NTS ? 2 : 0;   // 2: the non-temporal bit
+#pragma unroll
+        for (int k = 0; k < KV; ++k) {
+            if (vec(blk, k) < nv) {
+                float xf[V], pf[V], nf[V], o[V], z[V];
+                unpack16<T>(xw[k], xf);
+                unpack16<T>(pw[k], pf);
+                unpack16<T>(nw[k], nf);
+#pragma unroll
+                for (int i = 0; i < V; ++i) apply_elem<2>(a, ratio, xf[i], pf[i], nf[i], o[i], z[i]);
+                const int off = (int)(vec(blk, k) * 16);
+                __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(o), ro, off, 0, kStoreAux);
+                if (a.pred_x0 != nullptr) __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(z), rz, off, 0, kStoreAux);
+            }
+        }
+    };
+
     if (blockIdx.x == nblk) {
         // wait for every data block's flag, sum their quads in a fixed order
-        // (the same bits on every call), publish the ratio. The flags this
-        // thread reads (i = threadIdx.x + j * kFuseBlock) all belong to slot
-        // threadIdx.x % 8.
+        // (the same bits on every call), publish the ratio. The blocks this
+        // thread looks at (i = threadIdx.x + j * kFuseBlock) all belong to
+        // slot threadIdx.x % 8.
         const uint64_t want = shared_load(&bar->slot[threadIdx.x % 8].epoch) + 1;
+        if (threadIdx.x < 8) want_s[threadIdx.x] = want;
         double t[4] = {0.0, 0.0, 0.0, 0.0};
         bool all = false;
         for (int it = 0; it < kFusePolls && !all; ++it) {
-            int mine = 1;
+            uint64_t f[NJ];
 #pragma unroll
-            for (int j = 0; j < kFuseMaxBlocks / kFuseBlock; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 // every flag load in flight at once: unconditional, indices
                 // past the last data block read its flag again and ignore it
                 // (its slot, and so its epoch, can differ from this thread's)
                 const unsigned i = threadIdx.x + j * kFuseBlock;
-                const uint64_t f = shared_load(&bar->flag[i < nblk ? i : nblk - 1]);
-                mine &= (i >= nblk) | (f == want);
+                f[j] = shared_load(&bar->flag[i < nblk ? i : nblk - 1]);
             }
-            all = __syncthreads_and(mine) != 0;
+            int missing = 0;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                missing += (threadIdx.x + j * kFuseBlock < nblk && f[j] != want) ? 1 : 0;
+            all = __syncthreads_and(missing == 0) != 0;
             if (!all) __builtin_amdgcn_s_sleep(1);
         }
         if (!all && threadIdx.x == 0) shared_store(&bar->err, want);
@@ -441,42 +507,56 @@ __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
         block_sum4<NW>(t, sh);
         if (threadIdx.x < 8) {
             const float r = ratio_of_sums(t, a.fuse_hi - a.fuse_lo, a.uniform != 0);
+            if (threadIdx.x == 0) ratio_s = r;
             __hip_atomic_store(&bar->slot[threadIdx.x].ratio, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             publish_after_stores();
             shared_store(&bar->slot[threadIdx.x].epoch, want);
+            publish_after_stores();   // the ratio is out before the leave marks are read
+        }
+        __syncthreads();
+        // blocks that stopped waiting before the ratio was out: leave marks
+        // four groups at a time (this block's scan is off the data blocks'
+        // path: they have the ratio), one ballot per wave and group
+#pragma unroll 4
+        for (int j = 0; j < NJ; ++j) {
+            const unsigned i = threadIdx.x + j * kFuseBlock;
+            const uint64_t m = shared_load(&bar->leave[i < nblk ? i : nblk - 1]);
+            const unsigned long long b = __ballot(i < nblk && m == want);
+            if ((threadIdx.x & 63) == 0) left_s[j][threadIdx.x >> 6] = b;
+        }
+        __syncthreads();
+        const float ratio = ratio_s;
+#pragma unroll 1
+        for (int j = 0; j < NJ; ++j) {
+#pragma unroll 1
+            for (int w = 0; w < NW; ++w) {
+                for (unsigned long long m = left_s[j][w]; m != 0; m &= m - 1) {   // block-uniform
+                    const unsigned blk = (unsigned)(j * kFuseBlock + w * 64 + __builtin_ctzll(m));
+                    __shared__ unsigned mine_s;
+                    if (threadIdx.x == 0) mine_s = claim_first(&bar->claim[blk], want_s[blk % 8]) ? 1u : 0u;
+                    __syncthreads();
+                    const bool take = mine_s != 0;
+                    __syncthreads();
+                    if (take) {
+                        u32x4 xw[KV], pw[KV], nw[KV];
+                        load_block(blk, xw, pw, nw);
+                        store_block(blk, ratio, xw, pw, nw);
+                    }
+                }
+            }
         }
         return;
     }
-    const int64_t nv = (a.fuse_hi - a.fuse_lo) / V;
-    // buffer descriptors over the segment: a 32-bit byte offset per vector
-    // serves the three tensors and the two outputs, and the descriptor's
-    // range check (on the offset register) makes loads past the segment read
-    // 0 and drops stores past it
-    const int bytes = (int)(nv * 16);
-    auto rsrc = [&](const void* p) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(static_cast<const T*>(p) + a.fuse_lo), 0, bytes,
-                                                 0x00020000);
-    };
-    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x), rp = rsrc(a.v_pos), rn = rsrc(a.v_neg);
-    const int blk0 = (int)blockIdx.x * kFuseBlock * KV;   // first vector of the block
-    auto voff = [&](int k) { return (blk0 + k * kFuseBlock + (int)threadIdx.x) * 16; };
+
     EulerSlot* sl = &bar->slot[blockIdx.x % 8];
     uint64_t e0 = 0;   // the slot's epoch at the launch
     if (threadIdx.x == 0) e0 = shared_load(&sl->epoch);
     u32x4 xw[KV], pw[KV], nw[KV];
-#pragma unroll
-    for (int k = 0; k < KV; ++k) {
-        // non-temporal (aux 2): each vector is read once (26.2 against 27.7 us
-        // with the default policy, config-5 latent)
-        xw[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, voff(k), 0, 2);
-        pw[k] = __builtin_amdgcn_raw_buffer_load_b128(rp, voff(k), 0, 2);
-        nw[k] = __builtin_amdgcn_raw_buffer_load_b128(rn, voff(k), 0, 2);
-    }
-    const int64_t my0 = blk0 + (int64_t)threadIdx.x;   // this thread's first vector
+    load_block(blockIdx.x, xw, pw, nw);
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
-        if (my0 + (int64_t)k * kFuseBlock < nv) {
+        if (vec(blockIdx.x, k) < nv) {
             float xf[V], pf[V], nf[V];
             unpack16<T>(xw[k], xf);
             unpack16<T>(pw[k], pf);
@@ -504,37 +584,32 @@ __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
     }
     if (threadIdx.x == 0) {
         bool done = false;
-        for (int it = 0; it < kFusePolls && !done; ++it) {
+        for (int it = 0; it < a.fuse_polls && !done; ++it) {
             done = shared_load(&sl->epoch) != e0;
             if (!done) __builtin_amdgcn_s_sleep(2);
         }
-        if (!done) shared_store(&bar->err, e0 + 1);
+        bool own = done;
+        if (!done) {
+            // leave the vectors to the reducing block; if the ratio is out by
+            // the time the mark is, take them back unless it has claimed them
+            shared_store(&bar->leave[blockIdx.x], e0 + 1);
+            publish_after_stores();   // the mark is out before the ratio is looked at again
+            done = shared_load(&sl->epoch) != e0;
+            own = done && claim_first(&bar->claim[blockIdx.x], e0 + 1);
+        }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        ratio_s = __hip_atomic_load(&sl->ratio, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        own_s = own ? 1u : 0u;
+        if (own) ratio_s = __hip_atomic_load(&sl->ratio, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+    if (own_s == 0) return;   // the reducing block stores this block's vectors
     const float ratio = ratio_s;
     // only the loaded words stay live across the barrier: the products the
     // statistics formed are formed again (kept, they would double the
     // registers a thread holds and halve the resident grid)
 #pragma unroll
     for (int k = 0; k < KV; ++k) asm volatile("" : "+v"(xw[k]), "+v"(pw[k]), "+v"(nw[k]));
-    const __amdgpu_buffer_rsrc_t ro = rsrc(a.x_prev);
-    const __amdgpu_buffer_rsrc_t rz = rsrc(a.pred_x0 != nullptr ? a.pred_x0 : a.x_prev);
-    constexpr int kStoreAux = T2H_EULER_NTS ? 2 : 0;   // 2: the non-temporal bit
-#pragma unroll
-    for (int k = 0; k < KV; ++k) {
-        if (my0 + (int64_t)k * kFuseBlock < nv) {
-            float xf[V], pf[V], nf[V], o[V], z[V];
-            unpack16<T>(xw[k], xf);
-            unpack16<T>(pw[k], pf);
-            unpack16<T>(nw[k], nf);
-#pragma unroll
-            for (int i = 0; i < V; ++i) apply_elem<2>(a, ratio, xf[i], pf[i], nf[i], o[i], z[i]);
-            __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(o), ro, voff(k), 0, kStoreAux);
-            if (a.pred_x0 != nullptr) __builtin_amdgcn_raw_buffer_store_b128(pack16<T>(z), rz, voff(k), 0, kStoreAux);
-        }
-    }
+    store_block(blockIdx.x, ratio, xw, pw, nw);
 }
 
 // Blocks of euler_fused_kernel<T, KV> resident at once on this device.
