@@ -316,8 +316,8 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
 //    call) and publishes it in 8 release slots, 128 bytes apart, which the
 //    data blocks poll in turn (block b polls slot b % 8);
 // 3. every data block applies the step to the vectors it holds and stores.
-// No two blocks update one word (same-address atomics from ~1,600 blocks
-// serialize). Each slot carries a 64-bit epoch: a launch reads it (e), its
+// In the normal course no two blocks update one word (same-address atomics
+// from ~1,600 blocks serialize). Each slot carries a 64-bit epoch: a launch reads it (e), its
 // blocks raise their flags to e + 1 and the reducing block sets the slot
 // to e + 1. Flags left by earlier launches hold at most e, so the
 // workspace needs no clearing and a graph replay reads the epoch the last
@@ -381,11 +381,11 @@ __device__ __forceinline__ u32x4 pack16(const float* f) {
     return w;
 }
 
-constexpr int kFusePolls = 1 << 20;
-
+constexpr int kFusePolls = 1 << 20;   // the reducing block's wait for the flags, at most
 
 // Every word the blocks of euler_fused_kernel share (partial quads, flags,
-// release slots) is written and read as a device-scope relaxed atomic: a
+// release slots, leave marks, claims) is written and read as a device-scope
+// relaxed atomic: a
 // device-coherent access that no XCD's L2 holds stale. The wave's own stores
 // are ordered by waiting for them before the store that publishes them (no
 // agent-scope fence: its L2 write-back and invalidate would run on every
