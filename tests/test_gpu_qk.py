@@ -201,14 +201,16 @@ def test_qk_errors(dev):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("h", [4, 6, 8, 12, 16])
 @pytest.mark.parametrize("source", ["coords", "grid", "table"])
-def test_16bit_head_groups_and_sources(dev, dtype, h, source):
-    """16-bit rows with head_dim 128 (config 5's storage): 1-4 groups of 4
-    heads per wave instruction, one with an idle tail (6 heads), 301 rows (a
-    partial last tile), the three position sources (int coords, the dense
-    grid index, a phase table), q and k biases, against the oracle; then q
-    alone in place, and the packed qkv with its v bias (bit-exact after one
-    rounding)."""
-    rows, d = 301, 128
+@pytest.mark.parametrize("d", [128, 64])
+def test_16bit_head_groups_and_sources(dev, dtype, h, source, d):
+    """16-bit rows: head_dim 128 (config 5's storage) in 1-4 groups of 4
+    heads per wave instruction (16 lanes a head), head_dim 64 (the SLat
+    DiT's) in 1-2 groups of 8 (8 lanes a head), with idle tails (6 or 12
+    heads), 301 rows (a partial last tile), the three position sources (int
+    coords, the dense grid index, a phase table), q and k biases, against
+    the oracle; then q alone in place, and the packed qkv with its v bias
+    (bit-exact after one rounding)."""
+    rows = 301
     q = storage_round(orc.randn(1000 + h, (rows, h, d)), dtype)
     k = storage_round(orc.randn(1001 + h, (rows, h, d)), dtype)
     gq, gk = _gammas(h, d, 1002 + h)

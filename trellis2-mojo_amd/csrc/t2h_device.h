@@ -242,6 +242,15 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// Sum over each half DPP row of 8 lanes (lanes 0-7, 8-15 of a row), every
+// lane of the half getting the same value.
+__device__ __forceinline__ float row8_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    return v;
+}
+
 // Sum over the whole wave64; result is wave-uniform.
 __device__ __forceinline__ float wave_sum(float v) {
     v = row16_sum(v);

@@ -43,16 +43,20 @@ constexpr int kSmallTileWaves = 4;         // ... when the launch is short of ro
 
 template <typename T, int D, int NG, int W, bool EARLY>
 __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab) {
-    using L = HeadLanes<T, D>;
+    // 16-bit rows with D = 64: a head over 8 lanes (16-byte pieces), 8 heads
+    // per wave instruction; otherwise 16 lanes, 4 heads
+    constexpr int LPH = (sizeof(T) == 2 && D == 64) ? 8 : 16;
+    constexpr int HPI = 64 / LPH;
+    using L = HeadLanes<T, D, LPH>;
     constexpr int E = L::E;
     constexpr int P = L::P;
     constexpr int VE = L::VE;
     constexpr int HALF = D / 2;
-    __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];   // gamma * scale
-    __shared__ __attribute__((aligned(16))) float bs[NG * 4 * D];   // bias (q, k or v)
+    __shared__ __attribute__((aligned(16))) float gs[NG * HPI * D];   // gamma * scale
+    __shared__ __attribute__((aligned(16))) float bs[NG * HPI * D];   // bias (q, k or v)
     const int lane = lane_id();
-    const int g = lane >> 4;
-    const int m = lane & 15;
+    const int g = lane / LPH;
+    const int m = lane % LPH;
     const int H = a.heads;
     const int HD = H * D;
     const int has_q = a.q_in != nullptr, has_k = a.k_in != nullptr;
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         float vv[NG][E];
 #pragma unroll
         for (int it = 0; it < NG; ++it) {
-            const int hh = 4 * it + g;
+            const int hh = HPI * it + g;
             L::load(vr + (int64_t)(hh < H ? hh : H - 1) * D, m, vv[it]);
         }
         for (int i = threadIdx.x; i < HD / 4; i += W * 64)
@@ -84,7 +88,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         if (!live) return;
 #pragma unroll
         for (int it = 0; it < NG; ++it) {
-            const int hh = 4 * it + g;
+            const int hh = HPI * it + g;
             if (hh < H) {
                 float bv[E];
                 L::params(&bs[hh * D], m, bv);
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
         }
 #pragma unroll
         for (int it = 0; it < NG; ++it) {
-            const int hh = 4 * it + g;
+            const int hh = HPI * it + g;
             if (hh < H) L::store(vr + (int64_t)hh * D, m, vv[it]);
         }
         return;
@@ -128,7 +132,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     // by a loop counter is placed in LDS (or scratch) by the compiler before
     // the loop is unrolled, and its store would wait for the parameter load
     // ahead of the row loads
-    constexpr int KP = (NG * D + W * 64 - 1) / (W * 64);   // parameter float4s per thread
+    constexpr int KP = (NG * HPI * D / 4 + W * 64 - 1) / (W * 64);   // parameter float4s per thread
     static_assert(KP <= 2, "parameter float4s per thread");
     const bool stage = gamma != nullptr || bias != nullptr;   // block-uniform
     const int pi0 = threadIdx.x, pi1 = threadIdx.x + W * 64;
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
     float v[NG][E];
 #pragma unroll
     for (int it = 0; it < NG; ++it) {
-        const int hh = 4 * it + g;
+        const int hh = HPI * it + g;
         const int hl = hh < H ? hh : H - 1;
         L::load(in + rl * a.in_stride + (int64_t)hl * D, m, v[it]);
     }
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
 
 #pragma unroll
     for (int it = 0; it < NG; ++it) {
-        const int hh = 4 * it + g;
+        const int hh = HPI * it + g;
         const bool valid = hh < H;
         if (bias != nullptr && valid) {
             float bv[E];
@@ -197,7 +201,9 @@ __global__ __launch_bounds__(W * 64) void qk_tile_kernel(QkArgs a, RopeSlots tab
             for (int i = 0; i < E; ++i) v[it][i] = add_rn(v[it][i], bv[i]);
         }
         if (gamma != nullptr) {
-            const float ss = row16_sum(sum_sq<E>(v[it]));
+            float ss = sum_sq<E>(v[it]);
+            if constexpr (LPH == 16) ss = row16_sum(ss);
+            else ss = row8_sum(ss);
             const float rn = ss < 1e-24f ? 1e12f : __builtin_amdgcn_rsqf(ss);
             float gv[E];
 #pragma unroll
@@ -347,11 +353,16 @@ hipError_t launch_fast(QkArgs a, const RopeSlots& tab, hipStream_t s) {
 
 template <typename T, int D>
 hipError_t launch_d(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
-    switch ((a.heads + 3) / 4) {
-        case 1: return launch_fast<T, D, 1>(a, tab, s);
-        case 2: return launch_fast<T, D, 2>(a, tab, s);
-        case 3: return launch_fast<T, D, 3>(a, tab, s);
-        default: return launch_fast<T, D, 4>(a, tab, s);
+    if constexpr (sizeof(T) == 2 && D == 64) {   // 8 heads per group (8 lanes per head)
+        if (a.heads <= 8) return launch_fast<T, D, 1>(a, tab, s);
+        return launch_fast<T, D, 2>(a, tab, s);
+    } else {
+        switch ((a.heads + 3) / 4) {
+            case 1: return launch_fast<T, D, 1>(a, tab, s);
+            case 2: return launch_fast<T, D, 2>(a, tab, s);
+            case 3: return launch_fast<T, D, 3>(a, tab, s);
+            default: return launch_fast<T, D, 4>(a, tab, s);
+        }
     }
 }
 
@@ -359,8 +370,10 @@ inline bool aligned_to(const void* p, int bytes) { return (reinterpret_cast<uint
 
 template <typename T>
 hipError_t launch_typed(const QkArgs& a, const RopeSlots& tab, hipStream_t s) {
-    // vector loads of min(16, E * sizeof(T)) bytes per lane need that alignment
-    const int E = a.head_dim / 16;
+    // vector loads of min(16, E * sizeof(T)) bytes per lane need that
+    // alignment (E = head_dim / lanes per head: 8 lanes for 16-bit D = 64)
+    const int lph = sizeof(T) == 2 && a.head_dim == 64 ? 8 : 16;
+    const int E = a.head_dim / lph;
     const int chunk = E * (int)sizeof(T) < 16 ? E * (int)sizeof(T) : 16;
     const int64_t ealign = chunk / (int64_t)sizeof(T);
     const bool aligned = (a.in_stride % ealign == 0) && (a.out_stride % ealign == 0) &&

@@ -75,18 +75,20 @@ __device__ __forceinline__ float sum_sq(const float* x) {
     return s;
 }
 
-// Lane layout of one head over the 16 lanes of a DPP row: lane m holds
-// E = D/16 elements as NC pieces of VE contiguous elements (16 bytes at
-// most), piece j at element j*16*VE + m*VE, so every load instruction reads
-// one contiguous span across the row (f32 with D = 128: two 16-byte pieces
-// 256 bytes apart). RoPE pairs (2p, 2p+1) stay inside one lane.
-template <typename T, int D>
+// Lane layout of one head over LPH lanes (16: a DPP row; 8: half a row):
+// lane m holds E = D/LPH elements as NC pieces of VE contiguous elements
+// (16 bytes at most), piece j at element j*LPH*VE + m*VE, so every load
+// instruction reads one contiguous span across the lanes (f32 with D = 128:
+// two 16-byte pieces 256 bytes apart). RoPE pairs (2p, 2p+1) stay inside
+// one lane.
+template <typename T, int D, int LPH = 16>
 struct HeadLanes {
-    static constexpr int E = D / 16;
+    static_assert(LPH == 16 || LPH == 8, "a head spans a DPP row or half of one");
+    static constexpr int E = D / LPH;
     static constexpr int VE = E * (int)sizeof(T) > 16 ? 16 / (int)sizeof(T) : E;
     static constexpr int NC = E / VE;
     static constexpr int P = E / 2;
-    __device__ static __forceinline__ int piece(int m, int j) { return j * 16 * VE + m * VE; }
+    __device__ static __forceinline__ int piece(int m, int j) { return j * LPH * VE + m * VE; }
     // element index of the lane's i-th value, and the slot of its pair t
     __device__ static __forceinline__ int elem(int m, int i) { return piece(m, i / VE) + i % VE; }
     __device__ static __forceinline__ int slot(int m, int t) { return elem(m, 2 * t) / 2; }
