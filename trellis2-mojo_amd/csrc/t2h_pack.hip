@@ -18,9 +18,10 @@
 //   outputs beyond 16 heads): a block of 4 waves takes 64 token rows of one
 //   tensor and loops over a group of heads; a wave instruction covers 4 rows
 //   of one head, the rows' cos/sin stay in registers across the heads. The
-//   transposed k goes through LDS (64 x (D+1) f32, odd row pitch:
-//   conflict-free column reads) and leaves as 16-byte vectors along the token
-//   axis.
+//   transposed k goes through LDS (f32: 64 x (D+1), odd row pitch,
+//   conflict-free column reads; 16-bit: the output bits in two 64 x (D+2)
+//   buffers, one per alternate head, so one barrier per head) and leaves as
+//   16-byte vectors along the token axis.
 // On MI355X the row-major k ([H, lp, D]) is the faster layout: its rows are
 // what an MFMA attention kernel reads as the K operand.
 //
@@ -96,7 +97,12 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
     using L = HeadLanes<T, D>;
     constexpr int E = L::E;
     constexpr int P = L::P;
-    __shared__ float tile[KT ? kPackRows : 1][KT ? D + 1 : 1];
+    // The transposed tile: f32 rows, one buffer (two barriers per head); for
+    // 16-bit storage the output bit patterns in two buffers, so a head's tile
+    // is written while the previous head's is read (one barrier per head).
+    constexpr bool kTwo = KT && sizeof(T) == 2;
+    __shared__ float tile[KT && !kTwo ? kPackRows : 1][KT && !kTwo ? D + 1 : 1];
+    __shared__ uint16_t tile2[kTwo ? 2 : 1][kTwo ? kPackRows : 1][kTwo ? D + 2 : 1];
     const int lane = lane_id();
     const int g = lane >> 4;
     const int m = lane & 15;
@@ -210,7 +216,16 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
 #pragma unroll
                 for (int i = 0; i < E; ++i) x[i] = 0.0f;
             }
-            if constexpr (KT) {
+            if constexpr (kTwo) {
+                // elements 2i, 2i+1 of a lane are adjacent (pieces of >= 2 elements)
+                const int tl = it * kPackRowsPerIter + wave * 4 + g;
+#pragma unroll
+                for (int i = 0; i < E; i += 2) {
+                    const uint32_t w = Word<T>::pack(x + i);
+                    tile2[zi & 1][tl][L::elem(m, i)] = (uint16_t)w;
+                    tile2[zi & 1][tl][L::elem(m, i) + 1] = (uint16_t)(w >> 16);
+                }
+            } else if constexpr (KT) {
                 const int tl = it * kPackRowsPerIter + wave * 4 + g;
 #pragma unroll
                 for (int i = 0; i < E; ++i) tile[tl][L::elem(m, i)] = round_to<T>(x[i]);
@@ -218,7 +233,26 @@ __global__ __launch_bounds__(kPackBlock) void pack_tile_kernel(PackArgs a, RopeS
                 L::store(out + ((int64_t)z * extent + t) * D, m, x);
             }
         }
-        if constexpr (KT) {
+        if constexpr (kTwo) {
+            // this head's tile is whole, and every read of the tile written
+            // two heads ago (the other buffer's previous contents) is done
+            __syncthreads();
+            if (zi + 1 < order.hpb) fetch(z + 1);
+            constexpr int VE = kPack<T>;
+            constexpr int VPR = kPackRows / VE;
+            for (int vi = threadIdx.x; vi < D * VPR; vi += kPackBlock) {
+                const int e = vi / VPR;
+                const int tq = (vi % VPR) * VE;
+                if (t0 + tq >= extent) continue;
+                uint16_t w[VE];
+#pragma unroll
+                for (int i = 0; i < VE; ++i) w[i] = tile2[zi & 1][tq + i][e];
+                u32x4 o;
+                __builtin_memcpy(&o, w, 16);
+                u32x4* dst = reinterpret_cast<u32x4*>(out + ((int64_t)z * D + e) * a.lp + t0 + tq);
+                if (T2H_NT) __builtin_nontemporal_store(o, dst); else *dst = o;
+            }
+        } else if constexpr (KT) {
             __syncthreads();
             if (zi + 1 < order.hpb) fetch(z + 1);
             constexpr int VE = kPack<T>;            // elements per 16-byte vector
