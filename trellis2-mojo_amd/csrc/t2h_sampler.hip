@@ -322,7 +322,11 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
 // to e + 1. Flags left by earlier launches hold at most e, so the
 // workspace needs no clearing and a graph replay reads the epoch the last
 // launch left; a first use on uninitialised memory is safe unless a word
-// happens to hold e + 1 (64-bit values: chance 2^-64 per word).
+// happens to hold e + 1 (64-bit values: chance 2^-64 per word). The ratio
+// goes out in the slot's release word, with the new epoch's low half, in
+// one 64-bit store; a data block waits for that word to differ from what it
+// read at its start (the epoch half always does), so one load brings it
+// the release and the ratio together.
 // The launcher sizes the grid to be resident at once (occupancy x CUs). A
 // grid that is not (other streams' kernels hold part of the GPU) still
 // finishes with the same result: a data block that has waited fuse_polls
@@ -335,10 +339,14 @@ __global__ __launch_bounds__(kEulerBlock) void euler_apply_kernel(EulerArgs a) {
 // bounded too (2^20 polls, about a second): past it, it sets `err` and goes
 // on, so the grid always drains.
 struct EulerSlot {
-    uint64_t epoch;   // e at the launch; e + 1 once `ratio` is out
-    float ratio;
-    unsigned pad[29];
+    uint64_t epoch;   // e at the launch, e + 1 after it
+    uint64_t word;    // the release word: low 32 bits of the epoch (high
+                      // half) and the ratio's bits (low half)
+    unsigned pad[28];
 };
+__device__ __forceinline__ uint64_t release_word(uint64_t epoch, float ratio) {
+    return ((uint64_t)(uint32_t)epoch << 32) | __builtin_bit_cast(uint32_t, ratio);
+}
 struct EulerBar {
     uint64_t err;     // set to e + 1 by the reducing block if it stopped waiting
     uint64_t pad[7];
@@ -508,8 +516,9 @@ __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
         if (threadIdx.x < 8) {
             const float r = ratio_of_sums(t, a.fuse_hi - a.fuse_lo, a.uniform != 0);
             if (threadIdx.x == 0) ratio_s = r;
-            __hip_atomic_store(&bar->slot[threadIdx.x].ratio, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            publish_after_stores();
+            // the ratio and the new epoch's low half in one 64-bit store:
+            // a block that sees the word change holds the ratio with it
+            shared_store(&bar->slot[threadIdx.x].word, release_word(want, r));
             shared_store(&bar->slot[threadIdx.x].epoch, want);
             publish_after_stores();   // the ratio is out before the leave marks are read
         }
@@ -549,8 +558,11 @@ __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
     }
 
     EulerSlot* sl = &bar->slot[blockIdx.x % 8];
-    uint64_t e0 = 0;   // the slot's epoch at the launch
-    if (threadIdx.x == 0) e0 = shared_load(&sl->epoch);
+    uint64_t e0 = 0, w0 = 0;   // the slot's epoch and release word at the launch
+    if (threadIdx.x == 0) {
+        e0 = shared_load(&sl->epoch);
+        w0 = shared_load(&sl->word);
+    }
     u32x4 xw[KV], pw[KV], nw[KV];
     load_block(blockIdx.x, xw, pw, nw);
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
@@ -584,8 +596,10 @@ __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
     }
     if (threadIdx.x == 0) {
         bool done = false;
+        uint64_t w = w0;
         for (int it = 0; it < a.fuse_polls && !done; ++it) {
-            done = shared_load(&sl->epoch) != e0;
+            w = shared_load(&sl->word);
+            done = w != w0;
             if (!done) __builtin_amdgcn_s_sleep(2);
         }
         bool own = done;
@@ -594,12 +608,13 @@ __global__ __launch_bounds__(kFuseBlock) void euler_fused_kernel(EulerArgs a) {
             // the time the mark is, take them back unless it has claimed them
             shared_store(&bar->leave[blockIdx.x], e0 + 1);
             publish_after_stores();   // the mark is out before the ratio is looked at again
-            done = shared_load(&sl->epoch) != e0;
+            w = shared_load(&sl->word);
+            done = w != w0;
             own = done && claim_first(&bar->claim[blockIdx.x], e0 + 1);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         own_s = own ? 1u : 0u;
-        if (own) ratio_s = __hip_atomic_load(&sl->ratio, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (own) ratio_s = __builtin_bit_cast(float, (uint32_t)w);
     }
     __syncthreads();
     if (own_s == 0) return;   // the reducing block stores this block's vectors
