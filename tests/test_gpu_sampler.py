@@ -166,7 +166,8 @@ def test_step_rescale_config5_latent(dev, dtype):
 
 # the workspace of the one-launch rescale: the barrier words (a 64-bit error
 # word in the first 64 bytes, 8 release slots of 128 bytes each starting with
-# a 64-bit epoch, then per block, for up to 2048 blocks, a 64-bit arrival
+# a 64-bit epoch and a 64-bit release word (the epoch's low half and the
+# ratio), then per block, for up to 2048 blocks, a 64-bit arrival
 # flag, leave mark and claim word), then one f64 quad per block
 FUSE_BYTES = 64 + 8 * 128 + 3 * 2048 * 8 + 2048 * 32
 
