@@ -96,6 +96,26 @@ def test_k_layouts_agree(dev, dtype, d):
     assert_close(kn[:, :rows].transpose(0, 1), host(kr), dtype, "packed k vs qk_rmsnorm_rope")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows", [25_000, 39_804, 100_000, 140_000])
+def test_k_transposed_head_groups(dev, dtype, rows):
+    """The transposed-k tile kernel walks a group of heads per block, the
+    16-bit tiles alternating between two LDS buffers from head to head. On
+    256 CUs these row counts give 2, 3, 6 and 12 heads per block; each must
+    equal the row-major layout (another kernel) exactly."""
+    h, d = 12, 128
+    g = torch.Generator(device=dev).manual_seed(rows)
+    qkv = torch.randn((rows, 3, h, d), generator=g, device=dev).to(dtype)
+    coords = torch.randint(0, 64, (rows, 4), generator=g, device=dev, dtype=torch.int32)
+    gq, gk = [torch.randn((h, d), generator=g, device=dev) * 0.05 + 1 for _ in range(2)]
+    bk = torch.randn((h, d), generator=g, device=dev) * 0.02
+    mp = pad64(rows)
+    kw = dict(bias_k=bk, gamma_q=gq, gamma_k=gk, freqs=nn.rope_freqs(d), coords=coords, mp=mp, lp=mp)
+    _, kt, _ = ops.attn_pack(None, qkv[:, 1], None, k_transposed=True, **kw)
+    _, kn, _ = ops.attn_pack(None, qkv[:, 1], None, k_transposed=False, **kw)
+    assert torch.equal(kt, kn.transpose(1, 2)), rows
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_cross_chain_q_only(dev, dtype):
     """Cross chain: q [rows, H, D] rows H*D apart, + bias, RMS, no RoPE, packed
