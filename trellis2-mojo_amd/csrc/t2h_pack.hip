@@ -13,7 +13,9 @@
 //   contiguous 16-byte lanes; each 16-lane DPP row holds one head (lane m:
 //   elements [m*E, m*E+E), E = D/16), so the per-head sum of squares is a
 //   4-step DPP row sum and one sincos per lane per row serves every head.
-//   Each head's rows land as contiguous runs of the head-major output.
+//   Each head's rows land as contiguous runs of the head-major output; for
+//   16-bit rows of head_dim 128 the block stages its rows in LDS and writes
+//   each head's run of 8 rows (2 KB) with whole 1 KB store instructions.
 // - pack_tile_kernel (the reference's transposed k [H, D, lp], and row-major
 //   outputs beyond 16 heads): a block of 4 waves takes 64 token rows of one
 //   tensor and loops over a group of heads; a wave instruction covers 4 rows
@@ -292,6 +294,10 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
     constexpr int KP = (NG * 4 * D + kRowBlock - 1) / kRowBlock;   // parameter values per thread
     __shared__ __attribute__((aligned(16))) float gs[NG * 4 * D];   // gamma * scale
     __shared__ __attribute__((aligned(16))) float bs[NG * 4 * D];   // bias
+    // 16-bit: the block's rows staged per head, then written as whole
+    // per-head runs of the tile's rows (kRowWaves * D * 2 bytes each)
+    constexpr bool kStage = sizeof(T) == 2 && VE * (int)sizeof(T) == 16 && L::NC == 1;
+    __shared__ __attribute__((aligned(16))) T ost[kStage ? kRowWaves : 1][kStage ? NG * 4 * D : 1];
     const int lane = lane_id();
     const int g = lane >> 4;
     const int m = lane & 15;
@@ -383,7 +389,7 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
         }
     }
     if (stage) lds_barrier();
-    if (r >= extent) return;
+    if (!kStage && r >= extent) return;
 
 #pragma unroll
     for (int it = 0; it < NG; ++it) {
@@ -425,7 +431,36 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
 #pragma unroll
             for (int i = 0; i < E; ++i) x[i] = 0.0f;
         }
-        L::store(out + ((int64_t)hh * extent + r) * D, m, x);
+        if constexpr (kStage) {
+            uint32_t w[VE / 2];
+#pragma unroll
+            for (int i = 0; i < VE / 2; ++i) w[i] = Word<T>::pack(x + 2 * i);
+            u32x4 o;
+            __builtin_memcpy(&o, w, 16);
+            *reinterpret_cast<u32x4*>(&ost[wave][hh * D + m * VE]) = o;
+        } else {
+            L::store(out + ((int64_t)hh * extent + r) * D, m, x);
+        }
+    }
+    if constexpr (kStage) {
+        lds_barrier();
+        // a pass of the block covers kRowBlock 16-byte vectors: whole runs
+        // of kRowWaves rows of kRowBlock * 16 / (kRowWaves * D * 2) heads
+        constexpr int VPR = D / VE;                  // vectors per head row
+        constexpr int VPH = VPR * kRowWaves;         // vectors per head run
+        constexpr int HPP = kRowBlock / VPH;         // heads per pass
+        static_assert(HPP * VPH == kRowBlock, "whole head runs per pass");
+        const int tr = (threadIdx.x % VPH) / VPR;    // row of the tile
+        const int tv = threadIdx.x % VPR;            // vector in the row
+        const int64_t rr = tile * kRowWaves + tr;
+#pragma unroll
+        for (int h0 = 0; h0 < NG * 4; h0 += HPP) {
+            const int hh = h0 + threadIdx.x / VPH;
+            if (hh < H && rr < extent) {
+                const u32x4 o = *reinterpret_cast<const u32x4*>(&ost[tr][hh * D + tv * VE]);
+                __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(out + ((int64_t)hh * extent + rr) * D + tv * VE));
+            }
+        }
     }
 }
 
