@@ -250,6 +250,32 @@ def test_16bit_head_groups_and_sources(dev, dtype, h, source, d):
     assert bits_equal(got[:, 2].contiguous(), (qkv[:, 2] + b3[2]).astype(np.float32), dtype), "v bias"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("res", [5, 12, 16, 1500])
+def test_dense_grid_sizes(dev, dtype, res):
+    """The dense-grid position source for grid sizes that are and are not
+    powers of two, one past 2^31 when cubed (R = 1500), over 3000 rows, so
+    the smaller grids wrap (row r sits at l = r % R^3), against the oracle
+    with the positions written out here (the oracle's grid for R <= 16 is
+    checked against them first)."""
+    rows, h, d = 3000, 12, 128
+    r = np.arange(rows, dtype=np.int64)
+    l = r % res ** 3
+    pos = np.stack([l // (res * res), (l // res) % res, l % res], axis=1).astype(np.float32)
+    if res <= 16:
+        assert np.array_equal(np.tile(orc.grid_positions(res), (rows // res ** 3 + 1, 1))[:rows], pos)
+    q = storage_round(orc.randn(1200 + res, (rows, h, d)), dtype)
+    k = storage_round(orc.randn(1201 + res, (rows, h, d)), dtype)
+    gq, gk = _gammas(h, d, 1202)
+    freqs = orc.rope_freqs(d)
+    phases = orc.rope_phases_from_positions(pos, d, freqs)
+    wq, wk = orc.qk_rms_rope(q, k, gq, gk, phases)
+    qo, ko = ops.qk_rmsnorm_rope(q=to_dev(q, dev, dtype), k=to_dev(k, dev, dtype), gamma_q=to_dev(gq, dev),
+                                 gamma_k=to_dev(gk, dev), freqs=freqs, grid_res=res)
+    assert_close(qo, wq, dtype, f"q {dtype} R={res}")
+    assert_close(ko, wk, dtype, f"k {dtype} R={res}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows", [2048, 2369])
 def test_reference_block_geometry(dev, dtype, rows):
