@@ -458,7 +458,8 @@ __global__ __launch_bounds__(kRowBlock) void pack_rows_kernel(PackArgs a, RopeSl
             const int hh = h0 + threadIdx.x / VPH;
             if (hh < H && rr < extent) {
                 const u32x4 o = *reinterpret_cast<const u32x4*>(&ost[tr][hh * D + tv * VE]);
-                __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(out + ((int64_t)hh * extent + rr) * D + tv * VE));
+                u32x4* dst = reinterpret_cast<u32x4*>(out + ((int64_t)hh * extent + rr) * D + tv * VE);
+                if (T2H_NT) __builtin_nontemporal_store(o, dst); else *dst = o;
             }
         }
     }
