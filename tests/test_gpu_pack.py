@@ -204,6 +204,31 @@ def test_many_heads_and_table_phases(dev, dtype):
         assert_close(vh, wv, dtype, f"vh {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_row_major_staged_mp_ne_lp(dev, dtype):
+    """16-bit head_dim 128 (the rows staged in LDS and written per head run)
+    with mp != lp, a ragged last tile and pads, both k layouts, against the
+    oracle; v bit-exact."""
+    rows, h, d = 1001, 12, 128
+    qkv = storage_round(orc.randn(2800, (rows, 3, h, d)), dtype)
+    bias, gq, gk = _params(h, d, 2801)
+    coords = np.zeros((rows, 4), np.int32)
+    coords[:, 1:] = orc.Rng(2802).uniform((rows, 3), 0, 64).astype(np.int32)
+    phases = orc.rope_phases_from_coords(coords, d, orc.rope_freqs(d))
+    mp, lp = pad64(rows), pad64(rows) + 64
+    wq, wk, wv = orc.attn_pack(qkv, h, d, mp, lp, bias.reshape(-1), gq, gk, phases)
+    q, k, v = _views(to_dev(qkv, dev, dtype), h, d)
+    b = to_dev(bias, dev)
+    for kt in (False, True):
+        qh, ko, vh = ops.attn_pack(q, k, v, mp=mp, lp=lp, bias_q=b[0], bias_k=b[1], bias_v=b[2],
+                                   gamma_q=to_dev(gq, dev), gamma_k=to_dev(gk, dev), freqs=nn.rope_freqs(d),
+                                   coords=to_dev(coords, dev), k_transposed=kt)
+        assert_close(qh, wq, dtype, f"qh {dtype}")
+        assert_close(ko if kt else ko.transpose(1, 2), wk, dtype, f"k transposed={kt} {dtype}")
+        assert torch.equal(vh.cpu(), torch.from_numpy(storage_round(wv, dtype)).to(dtype))
+        assert not host(qh)[:, rows:].any() and not host(vh)[:, rows:].any()
+
+
 def test_attn_pack_errors(dev):
     h, d = 4, 96
     x = torch.zeros((8, 3, h, d), device=dev)
