@@ -965,7 +965,8 @@ def main():
     # untimed for settle_ms of GPU time, then one window is timed whole
     # (steady) and one with an event pair around every op (in-chain per-op
     # durations; the events add a little to that window only).
-    steady = steady_state(torch, chain, args.settle_ms, max(args.steps, 30))
+    # five interleaved rounds: the leave-one-out differences are ~0.3 % of a window each
+    steady = steady_state(torch, chain, args.settle_ms, max(args.steps, 30), rounds=5)
     per_op = steady["per_op"]
     log(f"steady state after {steady['settle_ms']:.0f} ms of chain steps: {steady['us_per_step']:.1f} us/step, "
         f"{steady['gbs']:.1f} GB/s ({steady['pct_of_peak']:.1f}%); in-chain per-op sum "
