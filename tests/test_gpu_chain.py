@@ -18,7 +18,8 @@ the largest coordinate on each axis (angles up to 127 rad) and the largest
 coordinate sum, and 32 seeded random rows. Whole-tensor properties on top:
 the gated residual is bit-exact over all rows against single-rounding f32
 steps, and RoPE keeps each pair's norm (RMS-only output vs RMS + RoPE
-output). Metric and tolerances: tests/_parity.py (f16 storage: 2e-3).
+output). Metric and tolerances: tests/_parity.py (f16 storage: 2e-3, bf16:
+8e-3). The chain runs in f16 (the benchmark's storage) and again in bf16.
 """
 import numpy as np
 import pytest
@@ -30,11 +31,12 @@ from _parity import assert_close, bits_equal, host, max_err, storage_round
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def chain(dev):
+@pytest.fixture(scope="module", params=[torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def chain(dev, request):
     import bench
 
-    ch = bench.Chain(dev, torch.float16)
+    ch = bench.Chain(dev, request.param)
+    ch.dt = request.param
     assert ch.qo.data_ptr() == ch.q.data_ptr() and ch.gout.data_ptr() == ch.u.data_ptr()
     ch.x_in, ch.q_in, ch.k_in, ch.u_in = (t.clone() for t in (ch.x, ch.q, ch.k, ch.u))
     ch.temb = ch.op("timestep")()
@@ -78,15 +80,15 @@ def test_config5_ln_modulate_sampled_rows(chain):
     idx = _sample_rows(chain.coords_np)
     x = host(chain.x_in[idx])
     want = orc.ln_modulate(x, host(chain.shift), host(chain.scale), eps=1e-6)
-    assert_close(chain.h[idx], want, torch.float16, "config-5 LN + gathered modulate")
+    assert_close(chain.h[idx], want, chain.dt, "config-5 LN + gathered modulate")
 
 
 def test_config5_qk_rms_rope_sampled_rows(chain):
     idx = _sample_rows(chain.coords_np)
     ph = orc.rope_phases_from_coords(chain.coords_np[idx], chain.D, orc.rope_freqs(chain.D))
     wq, wk = orc.qk_rms_rope(host(chain.q_in[idx]), host(chain.k_in[idx]), host(chain.gq), host(chain.gk), ph)
-    assert_close(chain.qo[idx], wq, torch.float16, "config-5 q RMS + RoPE")
-    assert_close(chain.ko[idx], wk, torch.float16, "config-5 k RMS + RoPE")
+    assert_close(chain.qo[idx], wq, chain.dt, "config-5 q RMS + RoPE")
+    assert_close(chain.ko[idx], wk, chain.dt, "config-5 k RMS + RoPE")
 
 
 def test_config5_rope_keeps_pair_norms(chain):
@@ -101,38 +103,40 @@ def test_config5_rope_keeps_pair_norms(chain):
         n_rope = out.float().reshape(T, H, D // 2, 2).square().sum(-1).sqrt()
         n_rms = rms.float().reshape(T, H, D // 2, 2).square().sum(-1).sqrt()
         err = ((n_rope - n_rms).abs() / n_rms.clamp(min=1.0)).max().item()
-        assert err <= 2e-3, f"pair norm changed by RoPE: {err:.3e}"
+        tol = 2e-3 if chain.dt == torch.float16 else 8e-3
+        assert err <= tol, f"pair norm changed by RoPE: {err:.3e}"
         del rms, n_rope, n_rms
 
 
 def test_config5_gelu_sampled_rows(chain):
     idx = _sample_rows(chain.coords_np)
     want = orc.gelu_tanh_bias(host(chain.u_in[idx]), host(chain.bias))
-    assert_close(chain.gout[idx], want, torch.float16, "config-5 GELU-tanh + bias")
+    assert_close(chain.gout[idx], want, chain.dt, "config-5 GELU-tanh + bias")
 
 
 def test_config5_gated_residual(chain):
     """Sampled rows vs the oracle, and every row bit-exact against
     x + fl(y * gate) in f32 (two separate single-rounding torch ops, the
-    oracle's sequence) rounded once to f16."""
+    oracle's sequence) rounded once to the storage type."""
     idx = _sample_rows(chain.coords_np)
     want = orc.gate_residual(host(chain.x_in[idx]), host(chain.y[idx]), host(chain.gate),
                              offsets=np.array([0, len(idx)], np.int64))
-    assert bits_equal(chain.res[idx], storage_round(want, torch.float16), torch.float16)
+    assert bits_equal(chain.res[idx], storage_round(want, chain.dt), chain.dt)
     T = chain.T
     for lo in range(0, T, 65536):
         hi = min(T, lo + 65536)
         prod = torch.mul(chain.y[lo:hi].float(), chain.gate)
-        full = torch.add(chain.x_in[lo:hi].float(), prod).half()
+        full = torch.add(chain.x_in[lo:hi].float(), prod).to(chain.dt)
         assert torch.equal(chain.res[lo:hi].view(torch.int16), full.view(torch.int16)), f"rows {lo}:{hi}"
 
 
 def test_config5_max_err_report(chain):
-    """The largest per-op error on the sampled rows stays inside the f16
-    tolerance with margin (printed for the record)."""
+    """The largest per-op error on the sampled rows stays inside the
+    storage type's tolerance (printed for the record)."""
     idx = _sample_rows(chain.coords_np)
     x = host(chain.x_in[idx])
     e_ln = max_err(chain.h[idx], orc.ln_modulate(x, host(chain.shift), host(chain.scale), eps=1e-6))
     e_ge = max_err(chain.gout[idx], orc.gelu_tanh_bias(host(chain.u_in[idx]), host(chain.bias)))
-    print(f"config-5 max err: LN+mod {e_ln:.2e}, GELU {e_ge:.2e} (f16 tol 2e-3)", flush=True)
-    assert max(e_ln, e_ge) <= 2e-3
+    tol = 2e-3 if chain.dt == torch.float16 else 8e-3
+    print(f"config-5 {chain.dt} max err: LN+mod {e_ln:.2e}, GELU {e_ge:.2e} (tol {tol:.0e})", flush=True)
+    assert max(e_ln, e_ge) <= tol
